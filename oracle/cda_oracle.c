@@ -1,0 +1,448 @@
+/*
+ * CPU restatement of the reference CDA algorithm -- TEST INFRASTRUCTURE ONLY.
+ *
+ * Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may
+ * load this library, and only as the checker.  The product (sub0_amd/) never
+ * links or calls it.
+ *
+ * Reference functions restated here (file:line in the reference tree):
+ *   hadamard_matrix          cda/algorithm/compression.py:43-57
+ *   Compressor.rotate        cda/algorithm/compression.py:287-291
+ *   Compressor.quantize_unit cda/algorithm/compression.py:298-313
+ *   Compressor.encode        cda/algorithm/compression.py:315-335
+ *   pack_4bit / pack_2bit    cda/algorithm/compression.py:163-179, 375-386
+ *   Compressor.decode        cda/algorithm/compression.py:337-361
+ *   attention_reference      cda/algorithm/attention.py:60-93
+ *   attention_compressed     cda/algorithm/attention.py:426-482
+ *   attention_partial_reference / merge_partials  attention.py:190-272
+ *   causal_mask              cda/algorithm/attention.py:46-57
+ *
+ * Arithmetic contract of the encode (the rounding points follow the
+ * reference exactly; the summation orders are pinned so that the HIP kernel
+ * reproduces every bit):
+ *   1. S_j = sum_i x_i * sign(H_ij) in float64.  Inputs are float16, so every
+ *      partial sum is exact and the order does not matter.
+ *   2. y_j = S_j * h32 in float64, h32 = fp32(1/sqrt(128)) = 0x3db504f3 (the
+ *      entry value of the reference's fp32 Hadamard matrix).
+ *   3. x_rot_j = fp16(y_j), round-to-nearest-even from float64 (the
+ *      reference rounds its fp32 matmul result to the input dtype,
+ *      compression.py:291).
+ *   4. ss = sum_j x_rot_j^2 in float64 in the "lane tree" order:
+ *      p[l] = x[2l]^2 + x[2l+1]^2 for l in 0..63, then p[l] += p[l^m] for
+ *      m = 1, 2, 4, ..., 32.  norm = fp32(sqrt(ss)), then clamp_min(1e-12f).
+ *   5. x_unit = fp32(x_rot) / norm (IEEE fp32 division), clamp to [-1, 1]
+ *      with NaN passing through (torch.clamp_ semantics).
+ *   6. quantize exactly as compression.py:298-313 does in fp32:
+ *      upper = #{i : !(cb[i] >= x)} (torch.bucketize, right=False; NaN -> L),
+ *      upper = min(upper, L-1); lower = max(upper-1, 0);
+ *      idx = |cb[upper]-x| < |x-cb[lower]| ? upper : lower (ties -> lower).
+ *   7. pack MSB-first (4-bit: even dim in the high nibble; 2-bit: dim 4j at
+ *      bits 7:6).
+ * The reference computes step 1-2 with an MKL sgemm and step 4 with
+ * Tensor.norm, whose fp32 accumulation orders are not specified; where they
+ * round differently from the exact value the two can disagree in the last
+ * ulp, which flips an index only for values within ulps of a decision
+ * boundary.  tests/test_oracle_golden.py counts and classifies those cases.
+ */
+#include <math.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+#define D 128
+
+/* ---------------------------------------------------------------- fp16 -- */
+
+static float f16_to_f32(uint16_t h) {
+    uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+    uint32_t exp = (h >> 10) & 0x1Fu;
+    uint32_t man = h & 0x3FFu;
+    uint32_t bits;
+    if (exp == 0) {
+        if (man == 0) {
+            bits = sign;
+        } else { /* subnormal: value = man * 2^-24 */
+            float v = (float)man * 5.9604644775390625e-8f;
+            memcpy(&bits, &v, 4);
+            bits |= sign;
+        }
+    } else if (exp == 31) {
+        bits = sign | 0x7F800000u | (man << 13);
+    } else {
+        bits = sign | ((exp + 112u) << 23) | (man << 13);
+    }
+    float f;
+    memcpy(&f, &bits, 4);
+    return f;
+}
+
+/* Correctly rounded (nearest-even) float64 -> float16. */
+uint16_t cda_oracle_f64_to_f16(double v) {
+    uint64_t b;
+    memcpy(&b, &v, 8);
+    uint16_t sign = (uint16_t)((b >> 48) & 0x8000u);
+    int e = (int)((b >> 52) & 0x7FF);
+    uint64_t m = b & 0xFFFFFFFFFFFFFull;
+    if (e == 0x7FF) return (uint16_t)(sign | 0x7C00u | (m ? 0x200u : 0u));
+    if (e == 0 && m == 0) return sign;
+    /* value = (1.m) * 2^(e-1023) for normal doubles (double subnormals are
+       far below the fp16 range and round to zero). */
+    if (e == 0) return sign;
+    int ue = e - 1023;                    /* unbiased exponent */
+    uint64_t sig = m | (1ull << 52);      /* 53-bit significand */
+    if (ue > 15) return (uint16_t)(sign | 0x7C00u);
+    int shift;                            /* bits to drop from sig */
+    uint16_t hexp;
+    if (ue >= -14) {                      /* normal fp16 */
+        shift = 52 - 10;
+        hexp = (uint16_t)(ue + 15);
+    } else {                              /* subnormal fp16: unit 2^-24 */
+        shift = 52 - 10 + (-14 - ue);
+        hexp = 0;
+        if (shift > 63) return sign;
+    }
+    uint64_t kept = sig >> shift;
+    uint64_t rem = sig & ((1ull << shift) - 1);
+    uint64_t half = 1ull << (shift - 1);
+    if (rem > half || (rem == half && (kept & 1))) kept++;
+    uint32_t out;
+    if (hexp) {
+        /* kept has 11 bits incl. hidden one; carry may bump the exponent */
+        if (kept == (1ull << 11)) { kept >>= 1; hexp++; }
+        if (hexp >= 31) return (uint16_t)(sign | 0x7C00u);
+        out = ((uint32_t)hexp << 10) | (uint32_t)(kept & 0x3FFu);
+    } else {
+        out = (uint32_t)kept;             /* may round up into the first normal */
+    }
+    return (uint16_t)(sign | out);
+}
+
+uint16_t cda_oracle_f32_to_f16(float v) { return cda_oracle_f64_to_f16((double)v); }
+
+float cda_oracle_f16_to_f32(uint16_t h) { return f16_to_f32(h); }
+
+/* ----------------------------------------------------------- rotation -- */
+
+static const uint32_t H32_BITS = 0x3db504f3u;   /* fp32(1/sqrt(128)) */
+
+static double h32(void) {
+    float f;
+    memcpy(&f, &H32_BITS, 4);
+    return (double)f;
+}
+
+/* Exact Sylvester sign transform in float64: out_j = sum_i x_i sign(H_ij),
+   H_ij = (-1)^popcount(i & j) (compression.py:52-56). */
+static void fwht128_exact(const float *x, double *out) {
+    double t[D];
+    for (int i = 0; i < D; ++i) t[i] = (double)x[i];
+    for (int len = 1; len < D; len <<= 1)
+        for (int i = 0; i < D; i += 2 * len)
+            for (int j = i; j < i + len; ++j) {
+                double a = t[j], b = t[j + len];
+                t[j] = a + b;
+                t[j + len] = a - b;
+            }
+    memcpy(out, t, sizeof(t));
+}
+
+/* compression.py:43-57 -- the fp32 matrix the reference builds. */
+void cda_oracle_hadamard128(float *H) {
+    float h;
+    memcpy(&h, &H32_BITS, 4);
+    for (int i = 0; i < D; ++i)
+        for (int j = 0; j < D; ++j)
+            H[i * D + j] = (__builtin_popcount((unsigned)(i & j)) & 1) ? -h : h;
+}
+
+/* ----------------------------------------------------------- quantize -- */
+
+/* compression.py:298-313 in fp32, torch.bucketize(right=False) semantics. */
+static uint8_t quantize_one(float x, const float *cb, int L) {
+    int upper = 0;
+    for (int i = 0; i < L; ++i) upper += !(cb[i] >= x);
+    if (upper > L - 1) upper = L - 1;
+    int lower = upper - 1 < 0 ? 0 : upper - 1;
+    float du = fabsf(cb[upper] - x);
+    float dl = fabsf(x - cb[lower]);
+    return (uint8_t)(du < dl ? upper : lower);
+}
+
+void cda_oracle_quantize(const float *x, int64_t n, const float *cb, int L, uint8_t *idx) {
+    for (int64_t i = 0; i < n; ++i) idx[i] = quantize_one(x[i], cb, L);
+}
+
+/* ------------------------------------------------------------- encode -- */
+
+/* Encode `rows` vectors of 128 fp16 values (compression.py:315-335).
+   bits = 4 (16 levels) or 2 (4 levels).  packed: rows x (128*bits/8) bytes.
+   norm: rows fp32.  xrot (optional): rows x 128 fp16 bit patterns. */
+void cda_oracle_encode_rows(const uint16_t *x, int64_t rows, const float *cb, int L,
+                            uint8_t *packed, float *norm, uint16_t *xrot) {
+    const int bits = (L == 16) ? 4 : 2;
+    const int bpr = D * bits / 8;
+    const double hh = h32();
+#pragma omp parallel for schedule(static)
+    for (int64_t r = 0; r < rows; ++r) {
+        float xf[D];
+        double S[D];
+        uint16_t xr[D];
+        for (int i = 0; i < D; ++i) xf[i] = f16_to_f32(x[r * D + i]);
+        fwht128_exact(xf, S);
+        for (int j = 0; j < D; ++j) xr[j] = cda_oracle_f64_to_f16(S[j] * hh);
+        if (xrot) memcpy(xrot + r * D, xr, sizeof(xr));
+        double p[64];
+        for (int l = 0; l < 64; ++l) {
+            double a = (double)f16_to_f32(xr[2 * l]);
+            double b = (double)f16_to_f32(xr[2 * l + 1]);
+            p[l] = a * a + b * b;
+        }
+        for (int m = 1; m < 64; m <<= 1) {
+            double q[64];
+            for (int l = 0; l < 64; ++l) q[l] = p[l] + p[l ^ m];
+            memcpy(p, q, sizeof(p));
+        }
+        float nv = (float)sqrt(p[0]);
+        if (nv < 1e-12f) nv = 1e-12f;    /* clamp_min(1e-12); NaN passes */
+        norm[r] = nv;
+        uint8_t idx[D];
+        for (int j = 0; j < D; ++j) {
+            float u = f16_to_f32(xr[j]) / nv;
+            u = u < -1.0f ? -1.0f : (u > 1.0f ? 1.0f : u);
+            idx[j] = quantize_one(u, cb, L);
+        }
+        uint8_t *out = packed + r * bpr;
+        if (bits == 4) {
+            for (int j = 0; j < bpr; ++j) out[j] = (uint8_t)((idx[2 * j] << 4) | idx[2 * j + 1]);
+        } else {
+            for (int j = 0; j < bpr; ++j)
+                out[j] = (uint8_t)((idx[4 * j] << 6) | (idx[4 * j + 1] << 4) |
+                                   (idx[4 * j + 2] << 2) | idx[4 * j + 3]);
+        }
+    }
+}
+
+/* --------------------------------------------------------- decode rows -- */
+
+static void unpack_row(const uint8_t *p, int bits, uint8_t *idx) {
+    if (bits == 4) {
+        for (int j = 0; j < D / 2; ++j) { idx[2 * j] = p[j] >> 4; idx[2 * j + 1] = p[j] & 15; }
+    } else {
+        for (int j = 0; j < D / 4; ++j) {
+            idx[4 * j] = (p[j] >> 6) & 3; idx[4 * j + 1] = (p[j] >> 4) & 3;
+            idx[4 * j + 2] = (p[j] >> 2) & 3; idx[4 * j + 3] = p[j] & 3;
+        }
+    }
+}
+
+/* compression.py:337-361 with rotated=True: fp16(cb[idx] * norm), the
+   multiply in fp32. */
+static void decode_row(const uint8_t *p, float nrm, const float *cb, int bits, float *out) {
+    uint8_t idx[D];
+    unpack_row(p, bits, idx);
+    for (int j = 0; j < D; ++j) out[j] = f16_to_f32(cda_oracle_f32_to_f16(cb[idx[j]] * nrm));
+}
+
+void cda_oracle_decode_rows(const uint8_t *packed, const float *norm, int64_t rows,
+                            const float *cb, int L, uint16_t *out) {
+    const int bits = (L == 16) ? 4 : 2;
+    const int bpr = D * bits / 8;
+    for (int64_t r = 0; r < rows; ++r) {
+        float v[D];
+        decode_row(packed + r * bpr, norm[r], cb, bits, v);
+        for (int j = 0; j < D; ++j) out[r * D + j] = cda_oracle_f32_to_f16(v[j]);
+    }
+}
+
+/* ------------------------------------------------- paged decode attention -- */
+
+/* Slot layout (cda_attn_v2.py:20-27, generalised to 2-bit):
+   [K codes kb | V codes kb | K norm f32 | V norm f32 | pad], kb = 128*bits/8. */
+typedef struct {
+    const uint8_t *kv;
+    int64_t row_bytes;   /* H_kv * slot_bytes */
+    int slot_bytes;
+    int kb;
+    int bits;
+} cache_view;
+
+static const uint8_t *slot_ptr(const cache_view *c, int64_t slot, int h) {
+    return c->kv + slot * c->row_bytes + (int64_t)h * c->slot_bytes;
+}
+
+static float load_f32(const uint8_t *p) { float f; memcpy(&f, p, 4); return f; }
+
+/* q_rot = fp16(fp32(q @ R)) with the sum in float64 (compression.py:287-291). */
+static void rotate_q(const uint16_t *q, const float *R, float *qr) {
+    for (int j = 0; j < D; ++j) {
+        double s = 0.0;
+        for (int k = 0; k < D; ++k) s += (double)f16_to_f32(q[k]) * (double)R[k * D + j];
+        qr[j] = f16_to_f32(cda_oracle_f32_to_f16((float)s));
+    }
+}
+
+/* Attention of one query vector (rotated frame) over the keys [k0, k1) of
+   sequence b / kv head h.  Writes the split-K partial (attention.py:190-236):
+   o_un (128, float64 accum), m (natural-log domain), l.  Causal masking is
+   done by the caller through k1. */
+static void partial_one(const cache_view *c, const int32_t *bt_row, int block_size, int h,
+                        const float *qr, int k0, int k1, const float *cbK, const float *cbV,
+                        float scale, double *o_un, double *m_out, double *l_out) {
+    double m = -INFINITY, l = 0.0;
+    for (int j = 0; j < D; ++j) o_un[j] = 0.0;
+    if (k1 <= k0) { *m_out = m; *l_out = l; return; }
+    double *s = (double *)malloc(sizeof(double) * (size_t)(k1 - k0));
+    for (int t = k0; t < k1; ++t) {
+        int64_t slot = (int64_t)bt_row[t / block_size] * block_size + t % block_size;
+        const uint8_t *p = slot_ptr(c, slot, h);
+        float kd[D];
+        decode_row(p, load_f32(p + 2 * c->kb), cbK, c->bits, kd);
+        double acc = 0.0;
+        for (int j = 0; j < D; ++j) acc += (double)qr[j] * (double)kd[j];
+        s[t - k0] = acc * (double)scale;
+        if (s[t - k0] > m) m = s[t - k0];
+    }
+    for (int t = k0; t < k1; ++t) {
+        int64_t slot = (int64_t)bt_row[t / block_size] * block_size + t % block_size;
+        const uint8_t *p = slot_ptr(c, slot, h);
+        float vd[D];
+        decode_row(p + c->kb, load_f32(p + 2 * c->kb + 4), cbV, c->bits, vd);
+        double pr = exp(s[t - k0] - m);
+        l += pr;
+        for (int j = 0; j < D; ++j) o_un[j] += pr * (double)vd[j];
+    }
+    free(s);
+    *m_out = m;
+    *l_out = l;
+}
+
+/* Decode attention over a paged cache: the full oracle path of
+   attention_compressed (attention.py:426-482) for M_q = 1, i.e.
+   q_rot = fp16(q @ R); O_rot = fp16(softmax(q_rot K^T * scale) V);
+   out = fp16(O_rot @ R^T).  With rotated_io != 0 the rotations are skipped
+   (q is already rotated and out stays rotated).
+   q: (B, H_q, 128) fp16; out: (B, H_q, 128) fp16. */
+void cda_oracle_decode_paged(const uint16_t *q, const uint8_t *kv, int H_kv, int slot_bytes,
+                             int L, const int32_t *block_table, int max_blocks,
+                             const int32_t *seq_lens, int B, int H_q, int block_size,
+                             const float *cbK, const float *cbV, const float *R, float scale,
+                             int rotated_io, uint16_t *out) {
+    cache_view c;
+    c.kv = kv;
+    c.slot_bytes = slot_bytes;
+    c.row_bytes = (int64_t)H_kv * slot_bytes;
+    c.bits = (L == 16) ? 4 : 2;
+    c.kb = D * c.bits / 8;
+    const int g = H_q / H_kv;
+#pragma omp parallel for collapse(2) schedule(dynamic)
+    for (int b = 0; b < B; ++b)
+        for (int hq = 0; hq < H_q; ++hq) {
+            const uint16_t *qv = q + ((int64_t)b * H_q + hq) * D;
+            float qr[D];
+            if (rotated_io) {
+                for (int j = 0; j < D; ++j) qr[j] = f16_to_f32(qv[j]);
+            } else {
+                rotate_q(qv, R, qr);
+            }
+            double o[D], m, l;
+            partial_one(&c, block_table + (int64_t)b * max_blocks, block_size, hq / g, qr, 0,
+                        seq_lens[b], cbK, cbV, scale, o, &m, &l);
+            float orot[D];
+            double den = l > 1e-30 ? l : 1e-30;
+            for (int j = 0; j < D; ++j) orot[j] = f16_to_f32(cda_oracle_f32_to_f16((float)(o[j] / den)));
+            uint16_t *ov = out + ((int64_t)b * H_q + hq) * D;
+            if (rotated_io) {
+                for (int j = 0; j < D; ++j) ov[j] = cda_oracle_f32_to_f16(orot[j]);
+            } else {
+                for (int j = 0; j < D; ++j) {
+                    double s = 0.0;
+                    for (int k = 0; k < D; ++k) s += (double)orot[k] * (double)R[j * D + k];
+                    ov[j] = cda_oracle_f32_to_f16((float)s);
+                }
+            }
+        }
+}
+
+/* Split-K partials (attention.py:190-236, 349-384) for M_q = 1 in the rotated
+   frame: for each (b, hq) the keys [k0, min(k1, seq_len)).  o_un: (B,H_q,128)
+   fp32, m/l: (B,H_q) fp32, natural-log domain. */
+void cda_oracle_decode_partial(const uint16_t *q_rot, const uint8_t *kv, int H_kv, int slot_bytes,
+                               int L, const int32_t *block_table, int max_blocks,
+                               const int32_t *seq_lens, int B, int H_q, int block_size,
+                               const float *cbK, const float *cbV, float scale, int k0, int k1,
+                               float *o_un, float *m_out, float *l_out) {
+    cache_view c;
+    c.kv = kv;
+    c.slot_bytes = slot_bytes;
+    c.row_bytes = (int64_t)H_kv * slot_bytes;
+    c.bits = (L == 16) ? 4 : 2;
+    c.kb = D * c.bits / 8;
+    const int g = H_q / H_kv;
+    for (int b = 0; b < B; ++b)
+        for (int hq = 0; hq < H_q; ++hq) {
+            float qr[D];
+            for (int j = 0; j < D; ++j) qr[j] = f16_to_f32(q_rot[((int64_t)b * H_q + hq) * D + j]);
+            int e = k1 < seq_lens[b] ? k1 : seq_lens[b];
+            double o[D], m, l;
+            partial_one(&c, block_table + (int64_t)b * max_blocks, block_size, hq / g, qr, k0, e,
+                        cbK, cbV, scale, o, &m, &l);
+            for (int j = 0; j < D; ++j) o_un[((int64_t)b * H_q + hq) * D + j] = (float)o[j];
+            m_out[b * H_q + hq] = (float)m;
+            l_out[b * H_q + hq] = (float)l;
+        }
+}
+
+/* Causal varlen prefill over the paged cache (attention.py:60-93 with the
+   lower-right mask of :46-57): query token i of sequence b (cu_q[b] <= row <
+   cu_q[b+1], M_b = cu_q[b+1]-cu_q[b]) attends keys [0, seq_lens[b] - M_b + i].
+   q: (T, H_q, 128) fp16 unrotated; out: (T, H_q, 128) fp16 unrotated. */
+void cda_oracle_prefill_paged(const uint16_t *q, const int32_t *cu_q, const uint8_t *kv, int H_kv,
+                              int slot_bytes, int L, const int32_t *block_table, int max_blocks,
+                              const int32_t *seq_lens, int B, int H_q, int block_size,
+                              const float *cbK, const float *cbV, const float *R, float scale,
+                              uint16_t *out) {
+    cache_view c;
+    c.kv = kv;
+    c.slot_bytes = slot_bytes;
+    c.row_bytes = (int64_t)H_kv * slot_bytes;
+    c.bits = (L == 16) ? 4 : 2;
+    c.kb = D * c.bits / 8;
+    const int g = H_q / H_kv;
+    for (int b = 0; b < B; ++b) {
+        int M = cu_q[b + 1] - cu_q[b];
+        int off = seq_lens[b] - M;
+#pragma omp parallel for collapse(2) schedule(dynamic)
+        for (int i = 0; i < M; ++i)
+            for (int hq = 0; hq < H_q; ++hq) {
+                int64_t row = cu_q[b] + i;
+                float qr[D];
+                rotate_q(q + (row * H_q + hq) * D, R, qr);
+                double o[D], m, l;
+                int kend = off + i + 1;
+                if (kend > seq_lens[b]) kend = seq_lens[b];
+                partial_one(&c, block_table + (int64_t)b * max_blocks, block_size, hq / g, qr, 0,
+                            kend, cbK, cbV, scale, o, &m, &l);
+                float orot[D];
+                double den = l > 1e-30 ? l : 1e-30;
+                for (int j = 0; j < D; ++j)
+                    orot[j] = f16_to_f32(cda_oracle_f32_to_f16((float)(o[j] / den)));
+                uint16_t *ov = out + (row * H_q + hq) * D;
+                for (int j = 0; j < D; ++j) {
+                    double s = 0.0;
+                    for (int k = 0; k < D; ++k) s += (double)orot[k] * (double)R[j * D + k];
+                    ov[j] = cda_oracle_f32_to_f16((float)s);
+                }
+            }
+    }
+}
+
+void cda_oracle_set_threads(int n) {
+#ifdef _OPENMP
+    omp_set_num_threads(n > 0 ? n : 1);
+#else
+    (void)n;
+#endif
+}
