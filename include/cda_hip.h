@@ -1,0 +1,108 @@
+/*
+ * cda_hip.h -- C ABI of libcda_hip.so, the MI355X (gfx950) kernels of
+ * Compressed-Domain Attention (CDA).
+ *
+ * Every entry point takes plain device pointers, sizes and a hipStream_t
+ * passed as `void *` (NULL = the default stream), launches asynchronously on
+ * that stream, allocates nothing, and returns 0 on success or a negative
+ * CDA_E_* code; cda_hip_last_error() then describes the failure (the message
+ * is per thread).  Outputs are caller-allocated and written in place, as in
+ * the reference's pybind functions.  All kernels are graph-capturable.
+ *
+ * Layouts shared by all entry points
+ *   head_dim D = 128.
+ *   Paged cache: flat (num_slots, H_kv, slot_bytes) uint8, slot index =
+ *   block_table[b][t / block_size] * block_size + t % block_size.
+ *   Slot = [K codes kb | V codes kb | K norm fp32 | V norm fp32 | pad],
+ *   kb = D*bits/8: K4V4 (16 levels) kb=64, slot_bytes 144 (cda_attn_v2.py:20-60);
+ *   K2V2 (4 levels) kb=32, slot_bytes 80.  Codes are packed MSB-first
+ *   (compression.py:163-179, 375-386).  slot_bytes must be a multiple of 16.
+ *   fp16 tensors are IEEE binary16 (passed as `void *`).
+ */
+#ifndef CDA_HIP_H
+#define CDA_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+    CDA_OK = 0,
+    CDA_E_INVALID = -1,   /* bad argument (shape, size, alignment, null) */
+    CDA_E_HIP = -2,       /* HIP runtime error while launching */
+    CDA_E_WORKSPACE = -3, /* workspace too small */
+};
+
+/* Library version (major*10000 + minor*100 + patch) and last error text. */
+int cda_hip_version(void);
+const char *cda_hip_last_error(void);
+
+/* ---------------------------------------------------------------- decode --
+ * Replaces the reference pybind function
+ *   cda_decode_full_hmma_v3(Q, kv_cache, block_table, seq_lens, cb_K, cb_V,
+ *                           rotation_fp32, rotation_fp16, out, group_size,
+ *                           block_size, tile_N, max_seq_len, scale)
+ * bound by cda/kernels_cuda/wrappers.py:115-124 (module
+ * _v1_decode_hmma_k4v4_gs{4,8}, hmma_loader.py:27-32).
+ *
+ * q:            (B, H_q, 128) fp16, unrotated, contiguous.
+ * kv_cache:     paged cache (see above), num_slots rows.
+ * block_table:  (B, bt_stride) int32.       seq_lens: (B,) int32 (past + 1).
+ * cb_k, cb_v:   (levels,) fp32 codebooks, levels = 16 (K4V4) or 4 (K2V2).
+ * rot_f32:      (128, 128) fp32 rotation R; q_rot = fp16(q @ R) and
+ *               out = fp16(fp16(O_rot) @ R^T) (compression.py:287-296).
+ * rot_f16:      accepted for signature parity, not read.
+ * out:          (B, H_q, 128) fp16, written in place.
+ * group_size:   H_q / H_kv, 4 or 8.
+ * tile_n:       context tokens per split-K partition; <= 0 selects the
+ *               MI355X default (cda_decode_plan).  Rounded up to 32.
+ * max_seq_len:  upper bound of seq_lens (sizes the split grid).
+ * workspace:    device scratch of at least cda_decode_workspace_size(...)
+ *               bytes, 256-byte aligned.
+ */
+int cda_decode_plan(int B, int H_q, int H_kv, int max_seq_len, int tile_n, int *tile_n_out,
+                    int *n_splits_out);
+size_t cda_decode_workspace_size(int B, int H_q, int H_kv, int max_seq_len, int tile_n);
+int cda_decode_full_hmma_v3(const void *q, const void *kv_cache, int64_t num_slots,
+                            int slot_bytes, int H_kv, const int32_t *block_table,
+                            int bt_stride, const int32_t *seq_lens, const float *cb_k,
+                            const float *cb_v, int levels, const float *rot_f32,
+                            const void *rot_f16, void *out, int B, int H_q, int group_size,
+                            int block_size, int tile_n, int max_seq_len, float scale,
+                            void *workspace, size_t workspace_bytes, void *stream);
+
+/* Profiling hook, no counterpart in the reference: when both are non-NULL,
+ * later cda_decode_full_hmma_v3 calls on this thread record the two hipEvent_t
+ * on the launch stream immediately before and after the split-K kernel (the
+ * kernel that streams the cache), so a caller can time it alone.  Pass NULL,
+ * NULL to stop. */
+int cda_decode_set_timing_events(void *start_event, void *stop_event);
+
+/* ---------------------------------------------------------------- encode --
+ * Replaces the reference pybind function
+ *   cda_paged_encode_fused(K, V, slot_mapping, flat_cache, cb_K, cb_V)
+ * bound by cda/kernels_cuda/wrappers.py:153-156 (module
+ * _v1_paged_encode_fused, hmma_loader.py:35-37).
+ *
+ * k, v:          (T, H_kv, 128) fp16 unrotated, row stride k_stride/v_stride
+ *                elements between tokens (heads contiguous).
+ * slot_mapping:  (T,) int32; a negative slot (vLLM padding) is skipped.
+ * flat_cache:    (num_slots, H_kv, slot_bytes) uint8, written in place.
+ * cb_k, cb_v:    (levels,) fp32, levels = 16 (K4V4) or 4 (K2V2).
+ * Per (token, head, role): Hadamard-128 (exact float64 butterfly, one fp16
+ * rounding), fp32 L2 norm clamped to 1e-12, nearest centroid with ties to
+ * the lower index, MSB-first packing (compression.py:315-335).
+ */
+int cda_paged_encode_fused(const void *k, const void *v, int64_t k_stride, int64_t v_stride,
+                           const int32_t *slot_mapping, int64_t num_tokens, void *flat_cache,
+                           int64_t num_slots, int slot_bytes, int H_kv, const float *cb_k,
+                           const float *cb_v, int levels, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* CDA_HIP_H */

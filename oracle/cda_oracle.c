@@ -29,7 +29,8 @@
  *      compression.py:291).
  *   4. ss = sum_j x_rot_j^2 in float64 in the "lane tree" order:
  *      p[l] = x[2l]^2 + x[2l+1]^2 for l in 0..63, then p[l] += p[l^m] for
- *      m = 1, 2, 4, ..., 32.  norm = fp32(sqrt(ss)), then clamp_min(1e-12f).
+ *      m = 1, 2, 4, ..., 32.  norm = sqrt(ss) correctly rounded to fp32, then
+ *      clamp_min(1e-12f).
  *   5. x_unit = fp32(x_rot) / norm (IEEE fp32 division), clamp to [-1, 1]
  *      with NaN passing through (torch.clamp_ semantics).
  *   6. quantize exactly as compression.py:298-313 does in fp32:
@@ -175,6 +176,30 @@ void cda_oracle_quantize(const float *x, int64_t n, const float *cb, int L, uint
     for (int64_t i = 0; i < n; ++i) idx[i] = quantize_one(x[i], cb, L);
 }
 
+/* Correctly rounded fp32 square root of a float64 value: move an
+   approximation until the exact fp32 rounding midpoints (25-bit values whose
+   squares are exact in float64) bracket x; ties go to even.  The HIP encoder
+   uses the same procedure. */
+static float sqrt_f64_to_f32_rn(double x) {
+    if (!(x > 0.0)) return x == 0.0 ? 0.0f : NAN;
+    if (isinf(x)) return INFINITY;
+    float f = (float)sqrt(x);
+    for (int it = 0; it < 4; ++it) {
+        float up = nextafterf(f, INFINITY);
+        double mid = ((double)f + (double)up) * 0.5;
+        double mm = mid * mid;
+        uint32_t fb;
+        memcpy(&fb, &f, 4);
+        if (mm < x || (mm == x && (fb & 1))) { f = up; continue; }
+        float dn = nextafterf(f, 0.0f);
+        double midl = ((double)f + (double)dn) * 0.5;
+        double ml = midl * midl;
+        if (ml > x || (ml == x && (fb & 1))) { f = dn; continue; }
+        break;
+    }
+    return f;
+}
+
 /* ------------------------------------------------------------- encode -- */
 
 /* Encode `rows` vectors of 128 fp16 values (compression.py:315-335).
@@ -205,7 +230,7 @@ void cda_oracle_encode_rows(const uint16_t *x, int64_t rows, const float *cb, in
             for (int l = 0; l < 64; ++l) q[l] = p[l] + p[l ^ m];
             memcpy(p, q, sizeof(p));
         }
-        float nv = (float)sqrt(p[0]);
+        float nv = sqrt_f64_to_f32_rn(p[0]);
         if (nv < 1e-12f) nv = 1e-12f;    /* clamp_min(1e-12); NaN passes */
         norm[r] = nv;
         uint8_t idx[D];
@@ -284,33 +309,37 @@ static void rotate_q(const uint16_t *q, const float *R, float *qr) {
     }
 }
 
-/* Attention of one query vector (rotated frame) over the keys [k0, k1) of
-   sequence b / kv head h.  Writes the split-K partial (attention.py:190-236):
-   o_un (128, float64 accum), m (natural-log domain), l.  Causal masking is
-   done by the caller through k1. */
-static void partial_one(const cache_view *c, const int32_t *bt_row, int block_size, int h,
-                        const float *qr, int k0, int k1, const float *cbK, const float *cbV,
-                        float scale, double *o_un, double *m_out, double *l_out) {
+/* Decode the keys/values [k0, k1) of sequence b / kv head h into fp16-valued
+   float arrays (compression.py:337-361 with rotated=True). */
+static void decode_window(const cache_view *c, const int32_t *bt_row, int block_size, int h,
+                          int k0, int k1, const float *cbK, const float *cbV, float *K, float *V) {
+    for (int t = k0; t < k1; ++t) {
+        int64_t slot = (int64_t)bt_row[t / block_size] * block_size + t % block_size;
+        const uint8_t *p = slot_ptr(c, slot, h);
+        decode_row(p, load_f32(p + 2 * c->kb), cbK, c->bits, K + (int64_t)(t - k0) * D);
+        decode_row(p + c->kb, load_f32(p + 2 * c->kb + 4), cbV, c->bits, V + (int64_t)(t - k0) * D);
+    }
+}
+
+/* Attention of one rotated query over n decoded keys: the split-K partial of
+   attention.py:190-236 (o_un, m in the natural-log domain, l), float64
+   accumulation.  Causal masking is done by the caller through n. */
+static void partial_one(const float *qr, const float *K, const float *V, int n, float scale,
+                        double *o_un, double *m_out, double *l_out) {
     double m = -INFINITY, l = 0.0;
     for (int j = 0; j < D; ++j) o_un[j] = 0.0;
-    if (k1 <= k0) { *m_out = m; *l_out = l; return; }
-    double *s = (double *)malloc(sizeof(double) * (size_t)(k1 - k0));
-    for (int t = k0; t < k1; ++t) {
-        int64_t slot = (int64_t)bt_row[t / block_size] * block_size + t % block_size;
-        const uint8_t *p = slot_ptr(c, slot, h);
-        float kd[D];
-        decode_row(p, load_f32(p + 2 * c->kb), cbK, c->bits, kd);
+    if (n <= 0) { *m_out = m; *l_out = l; return; }
+    double *s = (double *)malloc(sizeof(double) * (size_t)n);
+    for (int t = 0; t < n; ++t) {
         double acc = 0.0;
+        const float *kd = K + (int64_t)t * D;
         for (int j = 0; j < D; ++j) acc += (double)qr[j] * (double)kd[j];
-        s[t - k0] = acc * (double)scale;
-        if (s[t - k0] > m) m = s[t - k0];
+        s[t] = acc * (double)scale;
+        if (s[t] > m) m = s[t];
     }
-    for (int t = k0; t < k1; ++t) {
-        int64_t slot = (int64_t)bt_row[t / block_size] * block_size + t % block_size;
-        const uint8_t *p = slot_ptr(c, slot, h);
-        float vd[D];
-        decode_row(p + c->kb, load_f32(p + 2 * c->kb + 4), cbV, c->bits, vd);
-        double pr = exp(s[t - k0] - m);
+    for (int t = 0; t < n; ++t) {
+        double pr = exp(s[t] - m);
+        const float *vd = V + (int64_t)t * D;
         l += pr;
         for (int j = 0; j < D; ++j) o_un[j] += pr * (double)vd[j];
     }
@@ -319,11 +348,27 @@ static void partial_one(const cache_view *c, const int32_t *bt_row, int block_si
     *l_out = l;
 }
 
+static void finish_row(const double *o, double l, const float *R, int rotated_io, uint16_t *ov) {
+    float orot[D];
+    double den = l > 1e-30 ? l : 1e-30;
+    for (int j = 0; j < D; ++j) orot[j] = f16_to_f32(cda_oracle_f32_to_f16((float)(o[j] / den)));
+    if (rotated_io) {
+        for (int j = 0; j < D; ++j) ov[j] = cda_oracle_f32_to_f16(orot[j]);
+    } else {
+        for (int j = 0; j < D; ++j) {
+            double acc = 0.0;
+            for (int k = 0; k < D; ++k) acc += (double)orot[k] * (double)R[j * D + k];
+            ov[j] = cda_oracle_f32_to_f16((float)acc);
+        }
+    }
+}
+
 /* Decode attention over a paged cache: the full oracle path of
    attention_compressed (attention.py:426-482) for M_q = 1, i.e.
    q_rot = fp16(q @ R); O_rot = fp16(softmax(q_rot K^T * scale) V);
    out = fp16(O_rot @ R^T).  With rotated_io != 0 the rotations are skipped
-   (q is already rotated and out stays rotated).
+   (q is already rotated and out stays rotated).  K and V of each (b, kv head)
+   are decoded once and shared by the GQA group, as the reference does.
    q: (B, H_q, 128) fp16; out: (B, H_q, 128) fp16. */
 void cda_oracle_decode_paged(const uint16_t *q, const uint8_t *kv, int H_kv, int slot_bytes,
                              int L, const int32_t *block_table, int max_blocks,
@@ -339,30 +384,27 @@ void cda_oracle_decode_paged(const uint16_t *q, const uint8_t *kv, int H_kv, int
     const int g = H_q / H_kv;
 #pragma omp parallel for collapse(2) schedule(dynamic)
     for (int b = 0; b < B; ++b)
-        for (int hq = 0; hq < H_q; ++hq) {
-            const uint16_t *qv = q + ((int64_t)b * H_q + hq) * D;
-            float qr[D];
-            if (rotated_io) {
-                for (int j = 0; j < D; ++j) qr[j] = f16_to_f32(qv[j]);
-            } else {
-                rotate_q(qv, R, qr);
-            }
-            double o[D], m, l;
-            partial_one(&c, block_table + (int64_t)b * max_blocks, block_size, hq / g, qr, 0,
-                        seq_lens[b], cbK, cbV, scale, o, &m, &l);
-            float orot[D];
-            double den = l > 1e-30 ? l : 1e-30;
-            for (int j = 0; j < D; ++j) orot[j] = f16_to_f32(cda_oracle_f32_to_f16((float)(o[j] / den)));
-            uint16_t *ov = out + ((int64_t)b * H_q + hq) * D;
-            if (rotated_io) {
-                for (int j = 0; j < D; ++j) ov[j] = cda_oracle_f32_to_f16(orot[j]);
-            } else {
-                for (int j = 0; j < D; ++j) {
-                    double s = 0.0;
-                    for (int k = 0; k < D; ++k) s += (double)orot[k] * (double)R[j * D + k];
-                    ov[j] = cda_oracle_f32_to_f16((float)s);
+        for (int h = 0; h < H_kv; ++h) {
+            int n = seq_lens[b];
+            float *K = (float *)malloc(sizeof(float) * (size_t)(n > 0 ? n : 1) * D);
+            float *V = (float *)malloc(sizeof(float) * (size_t)(n > 0 ? n : 1) * D);
+            decode_window(&c, block_table + (int64_t)b * max_blocks, block_size, h, 0, n, cbK,
+                          cbV, K, V);
+            for (int gi = 0; gi < g; ++gi) {
+                int hq = h * g + gi;
+                const uint16_t *qv = q + ((int64_t)b * H_q + hq) * D;
+                float qr[D];
+                if (rotated_io) {
+                    for (int j = 0; j < D; ++j) qr[j] = f16_to_f32(qv[j]);
+                } else {
+                    rotate_q(qv, R, qr);
                 }
+                double o[D], m, l;
+                partial_one(qr, K, V, n, scale, o, &m, &l);
+                finish_row(o, l, R, rotated_io, out + ((int64_t)b * H_q + hq) * D);
             }
+            free(K);
+            free(V);
         }
 }
 
@@ -382,16 +424,27 @@ void cda_oracle_decode_partial(const uint16_t *q_rot, const uint8_t *kv, int H_k
     c.kb = D * c.bits / 8;
     const int g = H_q / H_kv;
     for (int b = 0; b < B; ++b)
-        for (int hq = 0; hq < H_q; ++hq) {
-            float qr[D];
-            for (int j = 0; j < D; ++j) qr[j] = f16_to_f32(q_rot[((int64_t)b * H_q + hq) * D + j]);
+        for (int h = 0; h < H_kv; ++h) {
             int e = k1 < seq_lens[b] ? k1 : seq_lens[b];
-            double o[D], m, l;
-            partial_one(&c, block_table + (int64_t)b * max_blocks, block_size, hq / g, qr, k0, e,
-                        cbK, cbV, scale, o, &m, &l);
-            for (int j = 0; j < D; ++j) o_un[((int64_t)b * H_q + hq) * D + j] = (float)o[j];
-            m_out[b * H_q + hq] = (float)m;
-            l_out[b * H_q + hq] = (float)l;
+            int n = e - k0;
+            float *K = (float *)malloc(sizeof(float) * (size_t)(n > 0 ? n : 1) * D);
+            float *V = (float *)malloc(sizeof(float) * (size_t)(n > 0 ? n : 1) * D);
+            if (n > 0)
+                decode_window(&c, block_table + (int64_t)b * max_blocks, block_size, h, k0, e,
+                              cbK, cbV, K, V);
+            for (int gi = 0; gi < g; ++gi) {
+                int hq = h * g + gi;
+                float qr[D];
+                for (int j = 0; j < D; ++j)
+                    qr[j] = f16_to_f32(q_rot[((int64_t)b * H_q + hq) * D + j]);
+                double o[D], m, l;
+                partial_one(qr, K, V, n, scale, o, &m, &l);
+                for (int j = 0; j < D; ++j) o_un[((int64_t)b * H_q + hq) * D + j] = (float)o[j];
+                m_out[b * H_q + hq] = (float)m;
+                l_out[b * H_q + hq] = (float)l;
+            }
+            free(K);
+            free(V);
         }
 }
 
@@ -413,29 +466,29 @@ void cda_oracle_prefill_paged(const uint16_t *q, const int32_t *cu_q, const uint
     const int g = H_q / H_kv;
     for (int b = 0; b < B; ++b) {
         int M = cu_q[b + 1] - cu_q[b];
-        int off = seq_lens[b] - M;
+        int n = seq_lens[b];
+        int off = n - M;
+        for (int h = 0; h < H_kv; ++h) {
+            float *K = (float *)malloc(sizeof(float) * (size_t)(n > 0 ? n : 1) * D);
+            float *V = (float *)malloc(sizeof(float) * (size_t)(n > 0 ? n : 1) * D);
+            decode_window(&c, block_table + (int64_t)b * max_blocks, block_size, h, 0, n, cbK,
+                          cbV, K, V);
 #pragma omp parallel for collapse(2) schedule(dynamic)
-        for (int i = 0; i < M; ++i)
-            for (int hq = 0; hq < H_q; ++hq) {
-                int64_t row = cu_q[b] + i;
-                float qr[D];
-                rotate_q(q + (row * H_q + hq) * D, R, qr);
-                double o[D], m, l;
-                int kend = off + i + 1;
-                if (kend > seq_lens[b]) kend = seq_lens[b];
-                partial_one(&c, block_table + (int64_t)b * max_blocks, block_size, hq / g, qr, 0,
-                            kend, cbK, cbV, scale, o, &m, &l);
-                float orot[D];
-                double den = l > 1e-30 ? l : 1e-30;
-                for (int j = 0; j < D; ++j)
-                    orot[j] = f16_to_f32(cda_oracle_f32_to_f16((float)(o[j] / den)));
-                uint16_t *ov = out + (row * H_q + hq) * D;
-                for (int j = 0; j < D; ++j) {
-                    double s = 0.0;
-                    for (int k = 0; k < D; ++k) s += (double)orot[k] * (double)R[j * D + k];
-                    ov[j] = cda_oracle_f32_to_f16((float)s);
+            for (int i = 0; i < M; ++i)
+                for (int gi = 0; gi < g; ++gi) {
+                    int hq = h * g + gi;
+                    int64_t row = cu_q[b] + i;
+                    float qr[D];
+                    rotate_q(q + (row * H_q + hq) * D, R, qr);
+                    int kend = off + i + 1;
+                    if (kend > n) kend = n;
+                    double o[D], m, l;
+                    partial_one(qr, K, V, kend, scale, o, &m, &l);
+                    finish_row(o, l, R, 0, out + (row * H_q + hq) * D);
                 }
-            }
+            free(K);
+            free(V);
+        }
     }
 }
 

@@ -1,0 +1,222 @@
+"""ctypes binding of libcda_hip.so (the C ABI declared in include/cda_hip.h).
+
+torch is used only as device-memory and stream plumbing: tensors are passed
+as raw pointers plus sizes, on ``torch.cuda.current_stream()``.  There is no
+CPU fallback: if the library is missing, or a tensor is not on a GPU, the
+call raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import threading
+from pathlib import Path
+
+import torch  # noqa: F401  -- must be loaded first so libamdhip64 resolves to torch's runtime
+
+LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libcda_hip.so"
+
+# Exported symbols (kept in sync with include/cda_hip.h; tests check both).
+SYMBOLS = (
+    "cda_hip_version",
+    "cda_hip_last_error",
+    "cda_decode_plan",
+    "cda_decode_workspace_size",
+    "cda_decode_full_hmma_v3",
+    "cda_decode_set_timing_events",
+    "cda_paged_encode_fused",
+)
+
+
+class NativeMissing(ImportError):
+    """libcda_hip.so is not built (run ``python -m sub0_amd.build``)."""
+
+
+class CdaError(RuntimeError):
+    """A C-ABI entry point returned an error code."""
+
+
+_lock = threading.Lock()
+_lib = None
+
+_P = ctypes.c_void_p
+_I32 = ctypes.c_int
+_I64 = ctypes.c_int64
+_F32 = ctypes.c_float
+_SZ = ctypes.c_size_t
+
+
+def lib():
+    """Load (once) and return the ctypes handle of libcda_hip.so."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        if not LIB_PATH.is_file():
+            raise NativeMissing(
+                f"{LIB_PATH} not found; build it with `python -m sub0_amd.build` "
+                "(hipcc --offload-arch=gfx950)")
+        L = ctypes.CDLL(str(LIB_PATH))
+        L.cda_hip_version.restype = _I32
+        L.cda_hip_version.argtypes = []
+        L.cda_hip_last_error.restype = ctypes.c_char_p
+        L.cda_hip_last_error.argtypes = []
+        L.cda_decode_plan.restype = _I32
+        L.cda_decode_plan.argtypes = [_I32, _I32, _I32, _I32, _I32,
+                                      ctypes.POINTER(_I32), ctypes.POINTER(_I32)]
+        L.cda_decode_workspace_size.restype = _SZ
+        L.cda_decode_workspace_size.argtypes = [_I32, _I32, _I32, _I32, _I32]
+        L.cda_decode_full_hmma_v3.restype = _I32
+        L.cda_decode_full_hmma_v3.argtypes = [
+            _P, _P, _I64, _I32, _I32, _P, _I32, _P, _P, _P, _I32, _P, _P, _P,
+            _I32, _I32, _I32, _I32, _I32, _I32, _F32, _P, _SZ, _P]
+        L.cda_decode_set_timing_events.restype = _I32
+        L.cda_decode_set_timing_events.argtypes = [_P, _P]
+        L.cda_paged_encode_fused.restype = _I32
+        L.cda_paged_encode_fused.argtypes = [
+            _P, _P, _I64, _I64, _P, _I64, _P, _I64, _I32, _I32, _P, _P, _I32, _P]
+        _lib = L
+    return _lib
+
+
+def _check(rc: int, what: str) -> None:
+    if rc != 0:
+        msg = lib().cda_hip_last_error().decode(errors="replace")
+        if msg.startswith(what + ": "):
+            msg = msg[len(what) + 2:]
+        if rc == -1:
+            raise ValueError(f"{what}: {msg}")
+        raise CdaError(f"{what} failed ({rc}): {msg}")
+
+
+def _ptr(t: torch.Tensor | None):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _stream(device: torch.device):
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def _require_gpu(*ts: torch.Tensor) -> torch.device:
+    dev = ts[0].device
+    for t in ts:
+        if t.device.type != "cuda":
+            raise ValueError("CDA kernels run on the GPU only; got a tensor on " + str(t.device))
+        if t.device != dev:
+            raise ValueError(f"all tensors must be on one device ({t.device} vs {dev})")
+    return dev
+
+
+# ------------------------------------------------------------------ decode --
+
+def decode_plan(B: int, H_q: int, H_kv: int, max_seq_len: int, tile_n: int = 0):
+    tn, ns = _I32(0), _I32(0)
+    _check(lib().cda_decode_plan(B, H_q, H_kv, max_seq_len, tile_n, ctypes.byref(tn),
+                                 ctypes.byref(ns)), "cda_decode_plan")
+    return tn.value, ns.value
+
+
+def decode_workspace_size(B: int, H_q: int, H_kv: int, max_seq_len: int, tile_n: int = 0) -> int:
+    return int(lib().cda_decode_workspace_size(B, H_q, H_kv, max_seq_len, tile_n))
+
+
+def decode(q: torch.Tensor, kv_cache: torch.Tensor, block_table: torch.Tensor,
+           seq_lens: torch.Tensor, cb_k: torch.Tensor, cb_v: torch.Tensor,
+           rot_f32: torch.Tensor, rot_f16: torch.Tensor | None, out: torch.Tensor, *,
+           group_size: int, block_size: int, tile_n: int, max_seq_len: int, scale: float,
+           workspace: torch.Tensor | None = None) -> None:
+    """Split-K decode over the paged cache; ``out`` is written in place.
+
+    q (B, H_q, 128) fp16; kv_cache (num_slots, H_kv, slot_bytes) uint8;
+    block_table (B, W) int32; seq_lens (B,) int32; cb_* (16,) fp32;
+    rot_f32 (128, 128) fp32; out (B, H_q, 128) fp16.
+    """
+    dev = _require_gpu(q, kv_cache, block_table, seq_lens, cb_k, cb_v, rot_f32, out)
+    if q.dtype != torch.float16 or out.dtype != torch.float16:
+        raise TypeError("q and out must be fp16")
+    if kv_cache.dtype != torch.uint8:
+        raise TypeError("kv_cache must be uint8")
+    if block_table.dtype != torch.int32 or seq_lens.dtype != torch.int32:
+        raise TypeError("block_table and seq_lens must be int32")
+    if cb_k.dtype != torch.float32 or cb_v.dtype != torch.float32 or rot_f32.dtype != torch.float32:
+        raise TypeError("codebooks and rot_f32 must be fp32")
+    if q.dim() != 3 or q.shape[-1] != 128 or not q.is_contiguous():
+        raise ValueError("q must be a contiguous (B, H_q, 128) tensor")
+    if out.shape != q.shape or not out.is_contiguous():
+        raise ValueError("out must be a contiguous tensor shaped like q")
+    if kv_cache.dim() != 3 or not kv_cache.is_contiguous():
+        raise ValueError("kv_cache must be a contiguous (num_slots, H_kv, slot_bytes) tensor")
+    if block_table.dim() != 2 or block_table.stride(1) != 1:
+        raise ValueError("block_table must be (B, max_blocks) with unit inner stride")
+    if rot_f32.shape != (128, 128) or not rot_f32.is_contiguous():
+        raise ValueError("rot_f32 must be a contiguous (128, 128) tensor")
+    if cb_k.numel() != cb_v.numel():
+        raise ValueError("cb_K and cb_V must have the same number of levels")
+    B, H_q, _ = q.shape
+    num_slots, H_kv, slot_bytes = kv_cache.shape
+    if block_table.shape[0] < B or seq_lens.numel() < B:
+        raise ValueError("block_table / seq_lens have fewer rows than q")
+    need = decode_workspace_size(B, H_q, H_kv, max_seq_len, tile_n)
+    if workspace is None or workspace.numel() < need or workspace.device != dev:
+        workspace = torch.empty(need + 256, dtype=torch.uint8, device=dev)
+    ws_ptr = workspace.data_ptr()
+    pad = (-ws_ptr) % 256
+    rc = lib().cda_decode_full_hmma_v3(
+        _ptr(q), _ptr(kv_cache), num_slots, slot_bytes, H_kv, _ptr(block_table),
+        block_table.stride(0), _ptr(seq_lens), _ptr(cb_k.contiguous()), _ptr(cb_v.contiguous()),
+        cb_k.numel(), _ptr(rot_f32), _ptr(rot_f16), _ptr(out), B, H_q, int(group_size),
+        int(block_size), int(tile_n), int(max_seq_len), float(scale),
+        ctypes.c_void_p(ws_ptr + pad), workspace.numel() - pad, _stream(dev))
+    _check(rc, "cda_decode_full_hmma_v3")
+
+
+def set_split_timing_events(start=None, stop=None) -> None:
+    """Record two ``torch.cuda.Event`` around the split-K kernel of later
+    decode calls on this thread (``None, None`` to stop)."""
+    sp = None if start is None else ctypes.c_void_p(start.cuda_event)
+    ep = None if stop is None else ctypes.c_void_p(stop.cuda_event)
+    _check(lib().cda_decode_set_timing_events(sp, ep), "cda_decode_set_timing_events")
+
+
+def decode_algorithmic_bytes(B: int, N: int, H_q: int = 32, H_kv: int = 8,
+                             block_size: int = 16, slot_data: int = 136) -> int:
+    """HBM bytes one decode step must move: codes + norms of every (token, KV
+    head), Q in and O out (fp16), the block-table entries and seq_lens."""
+    return (B * N * H_kv * slot_data + B * H_q * 128 * 2 * 2
+            + B * ((N + block_size - 1) // block_size) * 4 + 4 * B)
+
+
+# ------------------------------------------------------------------ encode --
+
+def paged_encode(k: torch.Tensor, v: torch.Tensor, slot_mapping: torch.Tensor,
+                 flat_cache: torch.Tensor, cb_k: torch.Tensor, cb_v: torch.Tensor) -> None:
+    """Fused Hadamard + norm + quantise + pack + scatter into ``flat_cache``."""
+    dev = _require_gpu(k, v, slot_mapping, flat_cache, cb_k, cb_v)
+    if k.dtype != torch.float16 or v.dtype != torch.float16:
+        raise TypeError("K, V must be fp16")
+    if flat_cache.dtype != torch.uint8:
+        raise TypeError("flat_cache must be uint8")
+    if slot_mapping.dtype != torch.int32:
+        raise TypeError("slot_mapping must be int32")
+    if k.dim() != 3 or k.shape != v.shape:
+        raise ValueError("K and V must be (T, H_kv, 128) tensors of one shape")
+    if k.shape[-1] != 128:
+        raise ValueError(f"D must be 128, got {k.shape[-1]}")
+    if k.stride(2) != 1 or k.stride(1) != 128 or v.stride(2) != 1 or v.stride(1) != 128:
+        raise ValueError("K and V need contiguous heads (stride (*, 128, 1))")
+    if flat_cache.dim() != 3 or not flat_cache.is_contiguous():
+        raise ValueError("flat_cache must be a contiguous (num_slots, H_kv, slot_bytes) tensor")
+    T, H_kv, _ = k.shape
+    if flat_cache.shape[1] != H_kv:
+        raise ValueError("flat_cache head count does not match K")
+    if slot_mapping.numel() < T:
+        raise ValueError("slot_mapping shorter than the number of tokens")
+    levels = cb_k.numel()
+    if cb_v.numel() != levels or levels not in (4, 16):
+        raise ValueError("cb_K and cb_V must both have 16 (K4V4) or 4 (K2V2) levels")
+    rc = lib().cda_paged_encode_fused(
+        _ptr(k), _ptr(v), k.stride(0), v.stride(0), _ptr(slot_mapping.contiguous()), T,
+        _ptr(flat_cache), flat_cache.shape[0], flat_cache.shape[2], H_kv,
+        _ptr(cb_k.float().contiguous()), _ptr(cb_v.float().contiguous()), levels, _stream(dev))
+    _check(rc, "cda_paged_encode_fused")

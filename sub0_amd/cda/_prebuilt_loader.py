@@ -1,0 +1,116 @@
+"""Loader for the MI355X CDA kernels (drop-in for ``cda/_prebuilt_loader.py``).
+
+The reference resolves each logical kernel name to a prebuilt CUDA ``.so``
+(``cda/_prebuilt_loader.py:56-80``).  Here every name resolves to one HIP
+library, ``sub0_amd/_lib/libcda_hip.so``, reached through its C ABI.
+``load_pybind_module(name)`` returns a module object whose attributes have
+the reference's positional signatures; ``load_torch_ops_library(name)``
+mirrors the TORCH_LIBRARY flavour.  Both are ``lru_cache``d and idempotent,
+and raise :class:`PrebuiltMissing` (an ``ImportError``) when the artefact is
+missing or the name is not provided, as the reference does
+(``_prebuilt_loader.py:41-53``).
+"""
+from __future__ import annotations
+
+import math
+import sys
+from functools import lru_cache
+from types import ModuleType
+
+import torch
+
+from sub0_amd import _native
+
+_DECODE_NAMES = {
+    "_v1_decode_hmma_k4v4_gs4": 4,
+    "_v1_decode_hmma_k4v4_gs8": 8,
+}
+
+
+class PrebuiltMissing(ImportError):
+    """Raised when no artefact matches the requested logical name."""
+
+
+def _lib_or_raise():
+    try:
+        return _native.lib()
+    except _native.NativeMissing as e:
+        raise PrebuiltMissing(str(e)) from e
+
+
+def _flat_cache(kv_cache: torch.Tensor) -> torch.Tensor:
+    """Accept (num_slots, H_kv, slot_w) or vLLM's (num_blocks, bs, H_kv, slot_w)."""
+    if kv_cache.dim() == 4:
+        nb, bs, h, w = kv_cache.shape
+        return kv_cache.view(nb * bs, h, w)
+    return kv_cache
+
+
+def _make_decode_module(name: str, gs: int) -> ModuleType:
+    mod = ModuleType(name)
+    mod.__doc__ = ("CDA split-K decode (K4V4, group size %d) on MI355X; replaces the "
+                   "reference's %s.so." % (gs, name))
+
+    def cda_decode_full_hmma_v3(Q, kv_cache, block_table, seq_lens, cb_K, cb_V,
+                                rotation_fp32, rotation_fp16, out, group_size, block_size,
+                                tile_N, max_seq_len, scale):
+        """Positional signature of the reference call (wrappers.py:115-124)."""
+        if int(group_size) != gs:
+            raise ValueError(f"{name} is built for group_size={gs}, got {group_size}")
+        _native.decode(Q, _flat_cache(kv_cache), block_table, seq_lens, cb_K, cb_V,
+                       rotation_fp32, rotation_fp16, out, group_size=gs,
+                       block_size=int(block_size), tile_n=int(tile_N),
+                       max_seq_len=int(max_seq_len),
+                       scale=float(scale) if scale is not None else 1.0 / math.sqrt(Q.shape[-1]))
+
+    mod.cda_decode_full_hmma_v3 = cda_decode_full_hmma_v3
+    return mod
+
+
+def _make_encode_module(name: str) -> ModuleType:
+    mod = ModuleType(name)
+    mod.__doc__ = "CDA fused paged encode (K4V4 and K2V2) on MI355X."
+
+    def cda_paged_encode_fused(K, V, slot_mapping, flat_cache, cb_K, cb_V):
+        """Positional signature of the reference call (wrappers.py:153-156)."""
+        _native.paged_encode(K, V, slot_mapping, _flat_cache(flat_cache), cb_K, cb_V)
+
+    mod.cda_paged_encode_fused = cda_paged_encode_fused
+    return mod
+
+
+def _factories():
+    f = {n: (lambda n=n, g=g: _make_decode_module(n, g)) for n, g in _DECODE_NAMES.items()}
+    f["_v1_paged_encode_fused"] = lambda: _make_encode_module("_v1_paged_encode_fused")
+    try:
+        from sub0_amd.cda.kernels_cuda import _prefill_modules
+    except ImportError:
+        _prefill_modules = None
+    if _prefill_modules is not None:
+        f.update(_prefill_modules.FACTORIES)
+    return f
+
+
+@lru_cache(maxsize=64)
+def load_pybind_module(name: str) -> ModuleType:
+    """Return the module object for logical kernel ``name``."""
+    fac = _factories().get(name)
+    if fac is None:
+        raise PrebuiltMissing(
+            f"Kernel module '{name}' is not provided by the MI355X build "
+            f"(available: {sorted(_factories())}).")
+    _lib_or_raise()
+    module = fac()
+    sys.modules[name] = module
+    return module
+
+
+@lru_cache(maxsize=64)
+def load_torch_ops_library(name: str):
+    """TORCH_LIBRARY flavour (reference ``_prebuilt_loader.py:69-80``)."""
+    try:
+        from sub0_amd.cda.kernels_vllm_fa2_fork import _ops
+    except ImportError as e:
+        raise PrebuiltMissing(f"torch.ops library '{name}' is not provided: {e}") from e
+    _lib_or_raise()
+    return _ops.namespace(name)

@@ -1,0 +1,132 @@
+"""Decode and encode entry points (drop-in for ``cda/kernels_cuda/wrappers.py``).
+
+* :func:`decode_hmma_v1` -- split-K decode over the paged K4V4 cache,
+  unrotated fp16 Q in, unrotated fp16 O written in place
+  (reference ``wrappers.py:79-124``).
+* :func:`paged_encode_fused_cuda` -- fused Hadamard + norm + quantise +
+  scatter into the paged cache (reference ``wrappers.py:127-156``); accepts
+  16-level (K4V4) and 4-level (K2V2) codebooks.
+
+Argument checks and error types follow the reference.  The split size
+(``_choose_tile_n``) is MI355X's own policy: it targets about four
+512-thread workgroups per CU (256 CUs) instead of the reference's
+2-blocks-per-SM rule, and it is what the kernel plans with when called
+through these wrappers.
+"""
+from __future__ import annotations
+
+import functools
+import math
+from typing import Optional
+
+import torch
+from torch import Tensor
+
+from sub0_amd import _native
+from sub0_amd.cda.kernels_cuda.hmma_loader import (
+    load_decode_hmma,
+    load_paged_encode_fused,
+)
+
+
+@functools.lru_cache(maxsize=8)
+def _get_num_sms(device_idx: int) -> int:
+    """Compute-unit count of the device (reference ``wrappers.py:35-38``)."""
+    return torch.cuda.get_device_properties(device_idx).multi_processor_count
+
+
+def _choose_tile_n(past_len: int, *, B: int = 1, H_q: int = 32, device_idx: int = 0,
+                   group_size: int = 4) -> int:
+    """Context tokens per split-K partition (reference ``wrappers.py:41-76``).
+
+    MI355X policy (``cda_decode_plan`` in the HIP library): one workgroup
+    covers 8 KV heads of one sequence; aim for ~4 workgroups per CU, at least
+    64 tokens and at most 512 partitions per sequence, rounded to 32 tokens.
+    ``device_idx`` is accepted for signature parity.
+    """
+    H_kv = max(1, H_q // group_size)
+    tile, _ = _native.decode_plan(B, H_q, H_kv, int(past_len), 0)
+    return tile
+
+
+def decode_hmma_v1(
+    Q_fp16: Tensor,           # (B, H_q, D) fp16 -- UNROTATED
+    kv_cache: Tensor,         # (num_total_slots, H_kv, 144) uint8 K4V4
+    block_table: Tensor,      # (B, max_blocks) int32
+    seq_lens: Tensor,         # (B,) int32 -- full seq_len (past + 1)
+    output: Tensor,           # (B, H_q, D) fp16 -- written in place
+    *,
+    cb_K: Tensor,
+    cb_V: Tensor,
+    rotation_fp32: Tensor,
+    rotation_fp16: Tensor,
+    group_size: int,
+    block_size: int,
+    scale: Optional[float] = None,
+    max_seq_len: Optional[int] = None,
+) -> None:
+    """Single-query split-K decode (K4V4), output written in place.
+
+    Graph-capturable when ``max_seq_len`` is given (no host sync); the split-K
+    workspace comes from the caching allocator on the current stream.
+    """
+    B, H_q, D = Q_fp16.shape
+    if scale is None:
+        scale = 1.0 / math.sqrt(D)
+    if max_seq_len is None:
+        max_seq_len = int(seq_lens.max().item())
+
+    mod = load_decode_hmma(k4v2=False, group_size=group_size)
+    tile_N = _choose_tile_n(max_seq_len, B=B, H_q=H_q,
+                            device_idx=Q_fp16.device.index or 0, group_size=group_size)
+    if Q_fp16.dtype != torch.float16:
+        Q_fp16 = Q_fp16.to(torch.float16)
+    if output.dtype != torch.float16:
+        raise ValueError("decode_hmma_v1 requires fp16 output buffer")
+
+    mod.cda_decode_full_hmma_v3(
+        Q_fp16.contiguous(),
+        kv_cache,
+        block_table.to(torch.int32) if block_table.dtype != torch.int32 else block_table,
+        seq_lens.to(torch.int32) if seq_lens.dtype != torch.int32 else seq_lens,
+        cb_K.float().contiguous(), cb_V.float().contiguous(),
+        rotation_fp32.float().contiguous(), rotation_fp16.contiguous(),
+        output,
+        group_size, block_size, tile_N, max_seq_len, scale,
+    )
+
+
+def paged_encode_fused_cuda(
+    K: Tensor,                      # (T, H_kv, D=128) fp16, UN-rotated
+    V: Tensor,
+    slot_mapping: Tensor,           # (T,) int32
+    flat_cache: Tensor,             # (num_slots, H_kv, slot_w) uint8
+    *,
+    cb_K: Tensor,                   # (16,) or (4,) fp32
+    cb_V: Tensor,
+) -> None:
+    """Fused Hadamard-128 + L2-norm + nearest-centroid + pack + paged scatter.
+
+    MSB-first packing, eps = 1e-12, negative slots skipped.  The kernel rotates
+    with an exact butterfly (no rotation argument), as the reference's does.
+    """
+    if K.dtype != torch.float16 or V.dtype != torch.float16:
+        raise TypeError("K, V must be fp16")
+    if flat_cache.dtype != torch.uint8:
+        raise TypeError("flat_cache must be uint8")
+    if K.shape[-1] != 128:
+        raise ValueError(f"D must be 128, got {K.shape[-1]}")
+    mod = load_paged_encode_fused()
+    sm_i32 = (slot_mapping
+              if slot_mapping.dtype == torch.int32
+              else slot_mapping.to(torch.int32))
+    mod.cda_paged_encode_fused(
+        K.contiguous(), V.contiguous(), sm_i32, flat_cache,
+        cb_K.float().contiguous(), cb_V.float().contiguous(),
+    )
+
+
+__all__ = [
+    "decode_hmma_v1",
+    "paged_encode_fused_cuda",
+]

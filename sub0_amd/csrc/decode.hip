@@ -1,0 +1,636 @@
+// Split-K flash-decode over the paged K4V4 codebook cache (gfx950).
+//
+// Reference contract: cda_decode_full_hmma_v3 as bound by
+// cda/kernels_cuda/wrappers.py:79-124; math of cda/algorithm/attention.py:
+// 426-482 (attention_compressed), split-K partials and merge of :190-272.
+//
+// Three launches on the caller's stream:
+//   1. rotate_q:  q_rot = fp16(q @ R) per (b, q-head); block (0,0) also writes
+//                 R^T into the workspace for the epilogue.
+//   2. split:     one workgroup per (b, context split, group of 8 KV heads);
+//                 wave w owns KV head 8*blockIdx.y + w and its GQA group.  Each
+//                 wave streams its split 32 tokens at a time straight from HBM
+//                 (K codes as one 16-byte load per lane per 16 tokens, V codes
+//                 and norms as dword loads) and dequantises through LDS tables
+//                 indexed by code byte, one table column per lane so reads do
+//                 not conflict.  K is rebuilt as fp16(centroid * norm) per
+//                 element exactly as the reference decodes it (the scores are
+//                 the precision-critical part); V uses fp16 centroids with the
+//                 V norm folded into P.  QK^T and PV run on MFMA
+//                 16x16x32 f16 with the GQA group as the N=16 side, and keeps
+//                 an exp2-domain online softmax.  It writes (O_unnorm, m, l).
+//   3. combine:   merges the splits (attention.py:239-272), rounds O_rot to
+//                 fp16 (attention.py:93), applies R^T (compression.py:293-296)
+//                 and writes fp16 out.
+#include "cda_common.h"
+
+#include <type_traits>
+
+namespace cda {
+
+namespace {
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+constexpr int kWaves = 8;                 // KV heads per workgroup
+constexpr int kThreads = 64 * kWaves;
+constexpr int kChunk = 32;                // tokens per inner iteration (2 MFMA tiles)
+// Dequant tables in LDS (128 KiB), one 256-byte row per code byte e:
+//   K at [0, 64 KiB):      e*256 + c*8, fp32 centroid pair, 32 lane columns
+//   V at [64 KiB, 128 KiB): 65536 + e*256 + c*4, fp16 centroid pair, 64 columns
+// Lane l reads K column (l & 31) and V column l, so reads never conflict, and
+// the byte address is one v_perm of the code byte with a per-lane constant
+// (byte 2 of that constant carries the 64 KiB bit of the V table).
+constexpr int kLutDwords = 2 * 256 * 64;
+constexpr float kLog2e = 1.4426950408889634f;
+
+struct SplitParams {
+    const uint16_t *q_rot;      // (B, H_q, 128) fp16
+    const uint8_t *kv;          // paged cache
+    const int32_t *block_table; // (B, bt_stride)
+    const int32_t *seq_lens;    // (B,)
+    const float *cb_k;
+    const float *cb_v;
+    float *part_o;              // (B, S, H_q, 128)
+    float *part_ml;             // (B, S, H_q, 2): m (log2 domain), l
+    int64_t row_bytes;          // H_kv * slot_bytes
+    int bt_stride;
+    int H_q;
+    int H_kv;
+    int slot_bytes;
+    int block_size;
+    int tile_n;
+    int n_splits;
+    float scale_log2;           // softmax scale * log2(e)
+};
+
+__device__ __forceinline__ uint32_t pack_h2(float lo, float hi) {
+    uint32_t a = (uint32_t)__half_as_ushort(__float2half_rn(lo));
+    uint32_t b = (uint32_t)__half_as_ushort(__float2half_rn(hi));
+    return a | (b << 16);
+}
+
+__device__ __forceinline__ floatx4 mfma16(uint4 a, uint4 b, floatx4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, a),
+                                                  __builtin_bit_cast(half8, b), c, 0, 0, 0);
+}
+
+// LDS table reads: byte address = code_byte * 256 + column offset.
+__device__ __forceinline__ uint32_t lut_at(const uint32_t *lut, uint32_t addr) {
+    return *reinterpret_cast<const uint32_t *>(reinterpret_cast<const char *>(lut) + addr);
+}
+
+__device__ __forceinline__ float2 lut2_at(const uint32_t *lut, uint32_t addr) {
+    return *reinterpret_cast<const float2 *>(reinterpret_cast<const char *>(lut) + addr);
+}
+
+// fp16(a), fp16(b) packed, round-to-nearest-even (v_cvt_pk_f16_f32 on gfx950).
+__device__ __forceinline__ uint32_t cvt_pk_rn(float a, float b) {
+    typedef float float2_ __attribute__((ext_vector_type(2)));
+    typedef _Float16 half2_ __attribute__((ext_vector_type(2)));
+    const half2_ h = __builtin_convertvector(float2_{a, b}, half2_);
+    return __builtin_bit_cast(uint32_t, h);
+}
+
+// Table address of code byte k of `w`: byte 0 <- col.byte0, byte 1 <- w.byte[k],
+// byte 2 <- col.byte2, byte 3 <- 0.
+template <int k>
+__device__ __forceinline__ uint32_t lut_addr(uint32_t w, uint32_t col) {
+    return __builtin_amdgcn_perm(w, col, 0x0C020400u | ((4u + k) << 8));
+}
+
+struct Chunk {
+    uint4 kq[2];        // K codes: token r16 of tile t, dims [32*q4, 32*q4+32)
+    float nk[2];        // K norm of token r16 of tile t
+    uint32_t vw[2][4];  // V codes: token 4*q4+i of tile t, dims [8*r16, 8*r16+8)
+    float nv[2][4];     // V norm of token 4*q4+i of tile t
+};
+
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+
+// Buffer descriptor over the 16 token rows of one tile (wave-uniform base in
+// SGPRs, so per-lane addressing is a constant 32-bit offset; reads past the
+// range return 0).
+__device__ __forceinline__ rsrc_t tile_rsrc(const uint8_t *base, int nbytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(base), 0, nbytes, 0x00020000);
+}
+
+struct LaneOffsets {
+    uint32_t k, nk, v[4], nv[4];
+};
+
+__device__ __forceinline__ void load_tile(Chunk &c, int t, rsrc_t r, const LaneOffsets &o) {
+    c.kq[t] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, o.k, 0, 0));
+    c.nk[t] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, o.nk, 0, 0));
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        c.vw[t][i] = __builtin_amdgcn_raw_buffer_load_b32(r, o.v[i], 0, 0);
+        c.nv[t][i] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, o.nv[i], 0, 0));
+    }
+}
+
+template <int GS>
+__global__ void __launch_bounds__(kThreads, 1)
+decode_split_kernel(SplitParams p) {
+    __shared__ __align__(16) uint32_t lds[kLutDwords];
+
+    const int sp = blockIdx.x;
+    const int b = blockIdx.z;
+    const int tid = threadIdx.x;
+
+    // ---- dequant tables (layout above).  K holds fp32 centroids: the decoded
+    // K is rounded to fp16 only after the norm multiply, as the reference
+    // decode does.
+    {
+        __shared__ float cbs[2][16];
+        if (tid < 32) cbs[tid >> 4][tid & 15] = (tid < 16) ? p.cb_k[tid] : p.cb_v[tid - 16];
+        __syncthreads();
+        for (int i = tid; i < kLutDwords / 2; i += kThreads) {
+            const int e = i >> 6;
+            lds[i] = __float_as_uint(cbs[0][(i & 1) ? (e & 15) : (e >> 4)]);
+            lds[kLutDwords / 2 + i] = pack_h2(cbs[1][e >> 4], cbs[1][e & 15]);
+        }
+        __syncthreads();
+    }
+
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // uniform per wave
+    const int lane = tid & 63;
+    const int h = blockIdx.y * kWaves + wave;
+    if (h >= p.H_kv) return;
+    const int r16 = lane & 15;
+    const int q4 = lane >> 4;
+
+    // Keys past the block-table row are never read, whatever seq_lens says.
+    const int seq_len =
+        __builtin_amdgcn_readfirstlane(min(p.seq_lens[b], p.bt_stride * p.block_size));
+    const int start = sp * p.tile_n;
+    const int end = min(start + p.tile_n, seq_len);
+    const int64_t part_row = ((int64_t)b * p.n_splits + sp) * p.H_q + (int64_t)h * GS;
+
+    if (start >= end) {
+        if (q4 == 0 && r16 < GS) {
+            p.part_ml[(part_row + r16) * 2 + 0] = -INFINITY;
+            p.part_ml[(part_row + r16) * 2 + 1] = 0.0f;
+        }
+        for (int i = lane; i < GS * kD; i += 64) p.part_o[part_row * kD + i] = 0.0f;
+        return;
+    }
+
+    // ---- query operand (B of QK^T): column g = r16, k slots = dims 32*q4+8*s+j.
+    // Columns g >= GS are zero; their scores are 0, so their (unused) rows of
+    // P and O stay finite.
+    uint4 qb[4];
+    {
+        const uint4 z = make_uint4(0, 0, 0, 0);
+        const uint16_t *qg = p.q_rot + ((int64_t)b * p.H_q + (int64_t)h * GS + r16) * kD + 32 * q4;
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+            qb[s] = (r16 < GS) ? *reinterpret_cast<const uint4 *>(qg + 8 * s) : z;
+    }
+
+    const uint32_t colK = (uint32_t)(lane & 31) * 8u;
+    const uint32_t colV = 0x10000u | ((uint32_t)lane * 4u);
+    const int KB = kD / 2;
+    LaneOffsets lo;
+    lo.k = (uint32_t)(r16 * p.row_bytes + q4 * 16);
+    lo.nk = (uint32_t)(r16 * p.row_bytes + 2 * KB);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        lo.v[i] = (uint32_t)((4 * q4 + i) * p.row_bytes + KB + 4 * r16);
+        lo.nv[i] = (uint32_t)((4 * q4 + i) * p.row_bytes + 2 * KB + 4);
+    }
+    const int32_t *bt = p.block_table + (int64_t)b * p.bt_stride;
+    const uint8_t *kvh = p.kv + (int64_t)h * p.slot_bytes;
+    const int bs = p.block_size;
+    const int tile_bytes = (int)(16 * p.row_bytes);
+
+    auto tile_res = [&](int t0) -> rsrc_t {
+        // The page id is wave-uniform: keep it (and the descriptor) in SGPRs.
+        const int page = __builtin_amdgcn_readfirstlane(bt[t0 / bs]);
+        const int64_t slot = (int64_t)page * bs + (t0 % bs);
+        return tile_rsrc(kvh + slot * p.row_bytes, tile_bytes);
+    };
+
+    auto load_chunk = [&](Chunk &c, int c0) {
+        const rsrc_t r0 = tile_res(c0);
+        const rsrc_t r1 = (c0 + 16 < end) ? tile_res(c0 + 16) : r0;
+        load_tile(c, 0, r0, lo);
+        load_tile(c, 1, r1, lo);
+    };
+
+    floatx4 acc_o[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc_o[j] = floatx4{0.f, 0.f, 0.f, 0.f};
+    float m_run = -INFINITY;   // running max of column g = r16 (log2 domain)
+    float l_run = 0.0f;        // lane-partial running sum
+
+    auto compute_chunk = [&](const Chunk &c, int c0, auto masked) {
+        constexpr bool MASK = decltype(masked)::value;
+        // ---- S = K Q^T: rows = 16 tokens of a tile, cols = GQA group.  The K
+        // operand is fp16(centroid * norm), bit-identical to the reference's
+        // decoded K (compression.py:355-359).
+        floatx4 sc[2];
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            floatx4 acc = {0.f, 0.f, 0.f, 0.f};
+            const uint32_t w[4] = {c.kq[t].x, c.kq[t].y, c.kq[t].z, c.kq[t].w};
+            const float nk = c.nk[t];
+#define CDA_K_PAIR(K_, W_)                                                     \
+    ({                                                                         \
+        const float2 cc = lut2_at(lds, lut_addr<K_>(W_, colK));               \
+        cvt_pk_rn(cc.x * nk, cc.y * nk);                                       \
+    })
+#pragma unroll
+            for (int s = 0; s < 4; ++s) {
+                uint4 a;
+                a.x = CDA_K_PAIR(0, w[s]);
+                a.y = CDA_K_PAIR(1, w[s]);
+                a.z = CDA_K_PAIR(2, w[s]);
+                a.w = CDA_K_PAIR(3, w[s]);
+                acc = mfma16(a, qb[s], acc);
+            }
+#undef CDA_K_PAIR
+            sc[t] = acc;
+        }
+        // ---- scores (log2 domain); only the last chunk of a split is masked.
+        float s2[2][4];
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                s2[t][i] = sc[t][i] * p.scale_log2;
+                if (MASK && c0 + 16 * t + 4 * q4 + i >= end) s2[t][i] = -INFINITY;
+            }
+        float cmax = fmaxf(fmaxf(fmaxf(s2[0][0], s2[0][1]), fmaxf(s2[0][2], s2[0][3])),
+                           fmaxf(fmaxf(s2[1][0], s2[1][1]), fmaxf(s2[1][2], s2[1][3])));
+        cmax = fmaxf(cmax, __shfl_xor(cmax, 16));
+        cmax = fmaxf(cmax, __shfl_xor(cmax, 32));
+        const float m_new = fmaxf(m_run, cmax);
+        const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);   // m_run = -inf -> 0
+        m_run = m_new;
+        // ---- P (A operand of PV): row g = r16, k slot j <-> (tile j/4, token 4*q4 + j%4).
+        float pv[2][4];
+        float psum = 0.0f;
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float pr = __builtin_amdgcn_exp2f(s2[t][i] - m_new);
+                psum += pr;
+                // A masked token weighs 0 (its V norm may be garbage).
+                pv[t][i] = (MASK && c0 + 16 * t + 4 * q4 + i >= end) ? 0.0f : pr * c.nv[t][i];
+            }
+        l_run = l_run * alpha + psum;
+        uint4 pa;
+        pa.x = cvt_pk_rn(pv[0][0], pv[0][1]);
+        pa.y = cvt_pk_rn(pv[0][2], pv[0][3]);
+        pa.z = cvt_pk_rn(pv[1][0], pv[1][1]);
+        pa.w = cvt_pk_rn(pv[1][2], pv[1][3]);
+        // ---- rescale O rows (row g = 4*q4 + i) when any group max moved.
+        float al[GS];
+        bool moved = false;
+#pragma unroll
+        for (int g = 0; g < GS; ++g) {
+            al[g] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(alpha), g));
+            moved |= (al[g] != 1.0f);
+        }
+        if (moved) {
+            float f[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                f[i] = 1.0f;
+#pragma unroll
+                for (int g = 0; g < GS; ++g)
+                    if (4 * q4 + i == g) f[i] = al[g];
+            }
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) acc_o[j][i] *= f[i];
+        }
+        // ---- V operand: column n = r16 of tile j holds dim 8*r16 + j; k slot
+        // pairs (2p, 2p+1) = tokens (4*q4 + 2*(p%2), +1) of tile p/2.  Pair two
+        // tokens' nibbles of one dim into one byte, then one table read gives
+        // both fp16 values.
+        uint32_t ev[4], od[4];
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int m2 = 0; m2 < 2; ++m2) {
+                const uint32_t wa = c.vw[t][2 * m2];
+                const uint32_t wb = c.vw[t][2 * m2 + 1];
+                ev[2 * t + m2] = (wa & 0xF0F0F0F0u) | ((wb >> 4) & 0x0F0F0F0Fu);
+                od[2 * t + m2] = ((wa << 4) & 0xF0F0F0F0u) | (wb & 0x0F0F0F0Fu);
+            }
+#define CDA_PV_TILE(K_, SRC_, J_)                                              \
+    {                                                                          \
+        uint4 vb;                                                              \
+        vb.x = lut_at(lds, lut_addr<K_>(SRC_[0], colV));                      \
+        vb.y = lut_at(lds, lut_addr<K_>(SRC_[1], colV));                      \
+        vb.z = lut_at(lds, lut_addr<K_>(SRC_[2], colV));                      \
+        vb.w = lut_at(lds, lut_addr<K_>(SRC_[3], colV));                      \
+        acc_o[J_] = mfma16(pa, vb, acc_o[J_]);                                 \
+    }
+        CDA_PV_TILE(0, ev, 0)
+        CDA_PV_TILE(0, od, 1)
+        CDA_PV_TILE(1, ev, 2)
+        CDA_PV_TILE(1, od, 3)
+        CDA_PV_TILE(2, ev, 4)
+        CDA_PV_TILE(2, od, 5)
+        CDA_PV_TILE(3, ev, 6)
+        CDA_PV_TILE(3, od, 7)
+#undef CDA_PV_TILE
+    };
+
+
+    // ---- main loop: three rotating buffers, loads run two chunks ahead; the
+    // chunk that reaches `end` is the only masked one.
+    Chunk ca, cb, cc;
+    int c0 = start;
+    load_chunk(ca, c0);
+    if (c0 + kChunk < end) load_chunk(cb, c0 + kChunk);
+#define CDA_STEP(CUR, NEXT2)                                                   \
+    {                                                                          \
+        if (c0 + 2 * kChunk < end) load_chunk(NEXT2, c0 + 2 * kChunk);         \
+        if (c0 + kChunk <= end) compute_chunk(CUR, c0, std::false_type{});              \
+        else compute_chunk(CUR, c0, std::true_type{});                                   \
+        c0 += kChunk;                                                          \
+        if (c0 >= end) break;                                                  \
+    }
+    while (true) {
+        CDA_STEP(ca, cc)
+        CDA_STEP(cb, ca)
+        CDA_STEP(cc, cb)
+    }
+#undef CDA_STEP
+
+    // ---- partials.
+    float l = l_run;
+    l += __shfl_xor(l, 16);
+    l += __shfl_xor(l, 32);
+    if (q4 == 0 && r16 < GS) {
+        p.part_ml[(part_row + r16) * 2 + 0] = m_run;
+        p.part_ml[(part_row + r16) * 2 + 1] = l;
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int g = 4 * q4 + i;
+        if (g < GS) {
+            float4 *dst = reinterpret_cast<float4 *>(p.part_o + (part_row + g) * kD + 8 * r16);
+            dst[0] = make_float4(acc_o[0][i], acc_o[1][i], acc_o[2][i], acc_o[3][i]);
+            dst[1] = make_float4(acc_o[4][i], acc_o[5][i], acc_o[6][i], acc_o[7][i]);
+        }
+    }
+}
+
+// q_rot[b, h, j] = fp16(sum_k fp32(q[b, h, k]) * R[k, j]).  The blocks also
+// share the transpose of R (one column per block per pass) for the epilogue.
+__global__ void __launch_bounds__(128)
+rotate_q_kernel(const uint16_t *q, const float *R, uint16_t *q_rot, float *RT, int H_q) {
+    __shared__ float qs[kD];
+    const int h = blockIdx.x, b = blockIdx.y, j = threadIdx.x;
+    const int64_t row = ((int64_t)b * H_q + h) * kD;
+    qs[j] = h2f(q[row + j]);
+    const int nblk = gridDim.x * gridDim.y;
+    for (int c = blockIdx.y * gridDim.x + blockIdx.x; c < kD; c += nblk)
+        RT[c * kD + j] = R[j * kD + c];
+    __syncthreads();
+    float acc = 0.0f;
+#pragma unroll 8
+    for (int k = 0; k < kD; ++k) acc = fmaf(qs[k], R[k * kD + j], acc);
+    q_rot[row + j] = __half_as_ushort(__float2half_rn(acc));
+}
+
+constexpr int kMaxSplits = 1024;
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int m = 1; m < 64; m <<= 1) v = fmaxf(v, __shfl_xor(v, m));
+    return v;
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int m = 1; m < 64; m <<= 1) v += __shfl_xor(v, m);
+    return v;
+}
+
+// Merge split partials (attention.py:239-272: m* = max m_i, weights
+// exp(m_i - m*), empty splits weigh 0, l clamped at 1e-30), round O_rot to
+// fp16 and unrotate with R^T.  One 128-thread block per (q-head, sequence);
+// the split loop is spread over the threads.
+__global__ void __launch_bounds__(128)
+combine_kernel(const float *part_o, const float *part_ml, const float *RT, uint16_t *out,
+               int H_q, int n_splits) {
+    __shared__ float orot[kD];
+    __shared__ float wts[kMaxSplits];
+    __shared__ float red[2];
+    const int h = blockIdx.x, b = blockIdx.y, j = threadIdx.x;
+    const int wave = j >> 6;
+    const int64_t base = (int64_t)b * n_splits * H_q + h;
+    float mx = -INFINITY;
+    for (int s = j; s < n_splits; s += kD) mx = fmaxf(mx, part_ml[(base + (int64_t)s * H_q) * 2]);
+    mx = wave_max(mx);
+    if ((j & 63) == 0) red[wave] = mx;
+    __syncthreads();
+    mx = fmaxf(red[0], red[1]);
+    __syncthreads();
+    float lp = 0.0f;
+    for (int s = j; s < n_splits; s += kD) {
+        const int64_t r = base + (int64_t)s * H_q;
+        const float ms = part_ml[r * 2];
+        const float w = (ms == -INFINITY) ? 0.0f : exp2f(ms - mx);
+        wts[s] = w;
+        if (w != 0.0f) lp += w * part_ml[r * 2 + 1];
+    }
+    lp = wave_sum(lp);
+    if ((j & 63) == 0) red[wave] = lp;
+    __syncthreads();
+    const float L = red[0] + red[1];
+    // Empty splits store zeros, so every partial can be read unconditionally
+    // (which lets the loads run ahead of the FMAs).
+    float o[4] = {0.f, 0.f, 0.f, 0.f};
+    const float *po = part_o + base * kD + j;
+    const int64_t step = (int64_t)H_q * kD;
+    int s = 0;
+    for (; s + 3 < n_splits; s += 4) {
+#pragma unroll
+        for (int u = 0; u < 4; ++u) o[u] += wts[s + u] * po[(int64_t)(s + u) * step];
+    }
+    for (; s < n_splits; ++s) o[0] += wts[s] * po[(int64_t)s * step];
+    const float v = ((o[0] + o[1]) + (o[2] + o[3])) / fmaxf(L, 1e-30f);
+    orot[j] = h2f(__half_as_ushort(__float2half_rn(v)));
+    __syncthreads();
+    float acc = 0.0f;
+#pragma unroll 8
+    for (int k = 0; k < kD; ++k) acc = fmaf(orot[k], RT[k * kD + j], acc);
+    out[((int64_t)b * H_q + h) * kD + j] = __half_as_ushort(__float2half_rn(acc));
+}
+
+struct WsLayout {
+    size_t q_rot, rt, part_o, part_ml, total;
+};
+
+WsLayout ws_layout(int B, int H_q, int n_splits) {
+    WsLayout w;
+    size_t off = 0;
+    w.q_rot = off;
+    off += align256((size_t)B * H_q * kD * 2);
+    w.rt = off;
+    off += align256((size_t)kD * kD * 4);
+    w.part_o = off;
+    off += align256((size_t)B * n_splits * H_q * kD * 4);
+    w.part_ml = off;
+    off += align256((size_t)B * n_splits * H_q * 2 * 4);
+    w.total = off;
+    return w;
+}
+
+// Optional profiling events recorded around the split kernel (per thread).
+thread_local hipEvent_t g_split_start = nullptr;
+thread_local hipEvent_t g_split_stop = nullptr;
+
+int num_cus() {
+    static int cached = 0;
+    if (!cached) {
+        int dev = 0, n = 0;
+        if (hipGetDevice(&dev) == hipSuccess &&
+            hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
+            n > 0)
+            cached = n;
+        else
+            cached = 256;
+    }
+    return cached;
+}
+
+}  // namespace
+
+}  // namespace cda
+
+using namespace cda;
+
+extern "C" int cda_decode_plan(int B, int H_q, int H_kv, int max_seq_len, int tile_n,
+                               int *tile_n_out, int *n_splits_out) {
+    (void)H_q;
+    if (B <= 0 || H_kv <= 0 || max_seq_len < 0)
+        return fail(CDA_E_INVALID, "cda_decode_plan: B, H_kv must be > 0 and max_seq_len >= 0");
+    const int n = max_seq_len > 0 ? max_seq_len : 1;
+    int tn;
+    if (tile_n > 0) {
+        tn = (tile_n + kChunk - 1) / kChunk * kChunk;
+    } else {
+        // Aim for ~4 workgroups per CU, splits of at least 64 tokens and at
+        // most 512 splits per sequence.
+        const int hg = (H_kv + kWaves - 1) / kWaves;
+        const int target = 4 * num_cus();
+        int splits = (target + B * hg - 1) / (B * hg);
+        const int max_by_len = (n + 63) / 64;
+        if (splits > max_by_len) splits = max_by_len;
+        if (splits > 512) splits = 512;
+        if (splits < 1) splits = 1;
+        tn = (n + splits - 1) / splits;
+        tn = (tn + kChunk - 1) / kChunk * kChunk;
+    }
+    if (tile_n_out) *tile_n_out = tn;
+    if (n_splits_out) *n_splits_out = (n + tn - 1) / tn;
+    return CDA_OK;
+}
+
+extern "C" size_t cda_decode_workspace_size(int B, int H_q, int H_kv, int max_seq_len,
+                                            int tile_n) {
+    int tn = 0, ns = 0;
+    if (cda_decode_plan(B, H_q, H_kv, max_seq_len, tile_n, &tn, &ns) != CDA_OK) return 0;
+    return ws_layout(B, H_q, ns).total;
+}
+
+extern "C" int cda_decode_full_hmma_v3(const void *q, const void *kv_cache, int64_t num_slots,
+                                       int slot_bytes, int H_kv, const int32_t *block_table,
+                                       int bt_stride, const int32_t *seq_lens, const float *cb_k,
+                                       const float *cb_v, int levels, const float *rot_f32,
+                                       const void *rot_f16, void *out, int B, int H_q,
+                                       int group_size, int block_size, int tile_n,
+                                       int max_seq_len, float scale, void *workspace,
+                                       size_t workspace_bytes, void *stream) {
+    (void)rot_f16;
+    (void)num_slots;
+    CDA_REQUIRE(q && kv_cache && block_table && seq_lens && cb_k && cb_v && rot_f32 && out,
+                "cda_decode_full_hmma_v3: null pointer argument");
+    CDA_REQUIRE(B > 0 && H_kv > 0 && H_q > 0, "cda_decode_full_hmma_v3: B, H_q, H_kv must be > 0");
+    CDA_REQUIRE(group_size == 4 || group_size == 8,
+                "cda_decode_full_hmma_v3: group_size must be 4 or 8");
+    CDA_REQUIRE(H_q == H_kv * group_size,
+                "cda_decode_full_hmma_v3: H_q must equal H_kv * group_size");
+    CDA_REQUIRE(levels == 16, "cda_decode_full_hmma_v3: the decode kernel reads K4V4 caches "
+                              "(16-level codebooks)");
+    CDA_REQUIRE(slot_bytes >= 2 * (kD / 2) + 8 && slot_bytes % 16 == 0,
+                "cda_decode_full_hmma_v3: slot_bytes must be >= 136 and a multiple of 16");
+    CDA_REQUIRE(block_size > 0 && block_size % 16 == 0,
+                "cda_decode_full_hmma_v3: block_size must be a positive multiple of 16");
+    CDA_REQUIRE(max_seq_len >= 0 && bt_stride > 0,
+                "cda_decode_full_hmma_v3: bad max_seq_len / block-table stride");
+    CDA_REQUIRE((int64_t)16 * H_kv * slot_bytes < (int64_t)1 << 31,
+                "cda_decode_full_hmma_v3: cache row too wide");
+    CDA_REQUIRE(((uintptr_t)kv_cache & 15) == 0 && ((uintptr_t)q & 15) == 0,
+                "cda_decode_full_hmma_v3: q and kv_cache must be 16-byte aligned");
+    int tn = 0, ns = 0;
+    int rc = cda_decode_plan(B, H_q, H_kv, max_seq_len, tile_n, &tn, &ns);
+    if (rc) return rc;
+    CDA_REQUIRE(ns <= kMaxSplits, "cda_decode_full_hmma_v3: tile_n gives more than 1024 "
+                                  "context splits; use a larger tile_n");
+    const WsLayout w = ws_layout(B, H_q, ns);
+    if (!workspace || workspace_bytes < w.total || ((uintptr_t)workspace & 255))
+        return fail(CDA_E_WORKSPACE, "cda_decode_full_hmma_v3: workspace missing, misaligned or "
+                                     "smaller than cda_decode_workspace_size()");
+    char *ws = static_cast<char *>(workspace);
+    hipStream_t st = static_cast<hipStream_t>(stream);
+
+    uint16_t *q_rot = reinterpret_cast<uint16_t *>(ws + w.q_rot);
+    float *RT = reinterpret_cast<float *>(ws + w.rt);
+    rotate_q_kernel<<<dim3(H_q, B), 128, 0, st>>>(static_cast<const uint16_t *>(q), rot_f32,
+                                                   q_rot, RT, H_q);
+    CDA_LAUNCH_CHECK("rotate_q_kernel");
+
+    SplitParams p;
+    p.q_rot = q_rot;
+    p.kv = static_cast<const uint8_t *>(kv_cache);
+    p.block_table = block_table;
+    p.seq_lens = seq_lens;
+    p.cb_k = cb_k;
+    p.cb_v = cb_v;
+    p.part_o = reinterpret_cast<float *>(ws + w.part_o);
+    p.part_ml = reinterpret_cast<float *>(ws + w.part_ml);
+    p.row_bytes = (int64_t)H_kv * slot_bytes;
+    p.bt_stride = bt_stride;
+    p.H_q = H_q;
+    p.H_kv = H_kv;
+    p.slot_bytes = slot_bytes;
+    p.block_size = block_size;
+    p.tile_n = tn;
+    p.n_splits = ns;
+    p.scale_log2 = scale * kLog2e;
+    dim3 grid(ns, (H_kv + kWaves - 1) / kWaves, B);
+    if (g_split_start && hipEventRecord(g_split_start, st) != hipSuccess)
+        return fail(CDA_E_HIP, "cda_decode_full_hmma_v3: hipEventRecord(start) failed");
+    if (group_size == 4)
+        decode_split_kernel<4><<<grid, kThreads, 0, st>>>(p);
+    else
+        decode_split_kernel<8><<<grid, kThreads, 0, st>>>(p);
+    CDA_LAUNCH_CHECK("decode_split_kernel");
+    if (g_split_stop && hipEventRecord(g_split_stop, st) != hipSuccess)
+        return fail(CDA_E_HIP, "cda_decode_full_hmma_v3: hipEventRecord(stop) failed");
+
+    combine_kernel<<<dim3(H_q, B), 128, 0, st>>>(p.part_o, p.part_ml, RT,
+                                                 static_cast<uint16_t *>(out), H_q, ns);
+    CDA_LAUNCH_CHECK("combine_kernel");
+    return CDA_OK;
+}
+
+extern "C" int cda_decode_set_timing_events(void *start_event, void *stop_event) {
+    CDA_REQUIRE((start_event == nullptr) == (stop_event == nullptr),
+                "cda_decode_set_timing_events: pass both events or neither");
+    g_split_start = static_cast<hipEvent_t>(start_event);
+    g_split_stop = static_cast<hipEvent_t>(stop_event);
+    return CDA_OK;
+}

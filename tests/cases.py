@@ -1,0 +1,61 @@
+"""Seeded CDA test cases shared by the GPU parity tests (uses the CPU checker)."""
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import numpy as np
+
+from oracle import cda_oracle as O
+from oracle import synth
+
+D = 128
+
+
+@dataclass
+class DecodeCase:
+    q: np.ndarray            # (B, H_q, 128) fp16
+    cache: np.ndarray        # (slots, H_kv, slot_bytes) uint8
+    block_table: np.ndarray  # (B, W) int32
+    seq_lens: np.ndarray     # (B,) int32
+    cb_k: np.ndarray
+    cb_v: np.ndarray
+    R: np.ndarray
+    H_kv: int
+    block_size: int
+    expected: np.ndarray     # oracle output (B, H_q, 128) fp16
+
+
+def make_decode_case(seed, seq_lens, *, H_kv=8, gs=4, block_size=16, cb=None, extra_blocks=3,
+                     scale=None, fill=0):
+    """Encode seeded K/V per sequence with the checker, scatter into a paged
+    cache through a permuted block table, and compute the checker's output."""
+    seq_lens = np.asarray(seq_lens, dtype=np.int32)
+    B = len(seq_lens)
+    H_q = H_kv * gs
+    if cb is None:
+        cb = synth_cb()
+    nmax = max(1, int(seq_lens.max()))
+    W = (nmax + block_size - 1) // block_size + extra_blocks
+    bt = synth.permuted_block_table(seed, B, W)
+    k = synth.kv_with_outliers(seed, (B, H_kv, nmax, D))
+    v = synth.normal_f16(seed + 1, (B, H_kv, nmax, D))
+    q = synth.normal_f16(seed + 2, (B, H_q, D))
+    kp, kn, _ = O.encode(k, cb)
+    vp, vn, _ = O.encode(v, cb)
+    cache = O.build_paged_cache(kp, kn, vp, vn, bt, block_size, cb.size,
+                                num_blocks=B * W, fill=fill)
+    R = O.hadamard128()
+    exp = O.decode_paged(q, cache, bt, seq_lens, cb, cb, R, H_kv=H_kv,
+                         block_size=block_size, scale=scale)
+    return DecodeCase(q, cache, bt, seq_lens, cb, cb, R, H_kv, block_size, exp)
+
+
+_CB = None
+
+
+def synth_cb():
+    global _CB
+    if _CB is None:
+        from pathlib import Path
+        _CB = np.load(Path(__file__).parent / "golden" / "codebooks.npz")["lloyd_beta16"]
+    return _CB

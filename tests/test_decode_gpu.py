@@ -1,0 +1,135 @@
+"""GPU parity of the split-K decode against the CPU checker (through the C ABI).
+
+Tolerance: 2e-3 max-abs on fp16 outputs against the fp32/fp64 checker run on
+the same compressed cache."""
+import json
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import cda_oracle as O
+from oracle import synth
+from tests.cases import make_decode_case
+
+pytestmark = pytest.mark.gpu
+TOL = 2e-3
+
+
+def run_gpu_decode(case, dev, *, gs, tile_n=0, max_seq_len=None, scale=None):
+    from sub0_amd import _native
+    q = torch.from_numpy(case.q.copy()).to(dev)
+    cache = torch.from_numpy(case.cache).to(dev)
+    bt = torch.from_numpy(case.block_table).to(dev)
+    sl = torch.from_numpy(case.seq_lens).to(dev)
+    cb = torch.from_numpy(case.cb_k).to(dev)
+    R = torch.from_numpy(case.R).to(dev)
+    out = torch.full_like(q, float("nan"))
+    msl = int(case.seq_lens.max()) if max_seq_len is None else max_seq_len
+    _native.decode(q, cache, bt, sl, cb, cb, R, R.half(), out, group_size=gs,
+                   block_size=case.block_size, tile_n=tile_n, max_seq_len=msl,
+                   scale=scale if scale is not None else 1.0 / np.sqrt(128))
+    torch.cuda.synchronize()
+    return out.cpu().numpy()
+
+
+def check(out, exp, tol=TOL):
+    assert np.isfinite(out).all(), "non-finite output"
+    err = np.abs(out.astype(np.float32) - exp.astype(np.float32)).max()
+    assert err <= tol, f"max abs err {err}"
+    return err
+
+
+CASES = [
+    # (name, seq_lens, H_kv, gs, block_size, tile_n, fill)
+    ("small_gqa", [300, 77], 2, 4, 16, 0, 0),
+    ("cfg0_shape", [4096], 8, 4, 16, 0, 0),
+    ("one_token", [1], 8, 4, 16, 0, 0xFF),
+    ("ragged", [33, 1000, 17, 2049], 8, 4, 16, 0, 0xFF),
+    ("gs8", [500, 1500], 8, 8, 16, 0, 0),
+    ("block32", [999, 64], 8, 4, 32, 0, 0xFF),
+    ("tile64", [2000], 8, 4, 16, 64, 0),
+    ("tile_big", [1500], 8, 4, 16, 4096, 0),
+    ("hkv4", [1234], 4, 4, 16, 0, 0),
+    ("hkv9", [700, 31], 9, 4, 16, 0, 0xFF),
+]
+
+
+@pytest.mark.parametrize("name,seq_lens,H_kv,gs,bs,tile_n,fill", CASES, ids=[c[0] for c in CASES])
+def test_decode_matches_checker(gpu, name, seq_lens, H_kv, gs, bs, tile_n, fill):
+    print(f"[decode] case={name} seq_lens={seq_lens} H_kv={H_kv} gs={gs} bs={bs}", flush=True)
+    case = make_decode_case(1000 + len(name), seq_lens, H_kv=H_kv, gs=gs, block_size=bs,
+                            fill=fill)
+    out = run_gpu_decode(case, gpu, gs=gs, tile_n=tile_n)
+    check(out, case.expected)
+
+
+def test_decode_scale_and_slack_max_seq_len(gpu):
+    """Non-default softmax scale; max_seq_len larger than every seq_len."""
+    case = make_decode_case(77, [400, 250], H_kv=8, gs=4, scale=0.3)
+    out = run_gpu_decode(case, gpu, gs=4, max_seq_len=1000, scale=0.3)
+    check(out, case.expected)
+
+
+def test_decode_empty_sequence_gives_zero(gpu):
+    case = make_decode_case(78, [0, 200], H_kv=8, gs=4)
+    out = run_gpu_decode(case, gpu, gs=4, max_seq_len=200)
+    assert np.all(out[0] == 0)
+    check(out[1:], case.expected[1:])
+
+
+def test_decode_golden_cfg0(gpu, golden, codebooks):
+    """BASELINE config 0 on the reference's own encoded cache and output."""
+    g = golden("attn_cfg0.npz")
+    meta = json.loads((__import__("pathlib").Path(__file__).parent / "golden" /
+                       "attn_cfg0.json").read_text())
+    B, H_kv, N = meta["B"], meta["H_kv"], meta["N"]
+    cb = codebooks["lloyd_beta16"]
+    bt = synth.permuted_block_table(meta["seed"], B, N // 16)
+    cache = O.build_paged_cache(g["k_idx"], g["k_norm"], g["v_idx"], g["v_norm"], bt, 16, 16)
+    from tests.cases import DecodeCase
+    R = codebooks["hadamard128"]
+    exp = O.decode_paged(g["q"][:, :, 0], cache, bt, np.full(B, N, np.int32), cb, cb, R,
+                         H_kv=H_kv, block_size=16)
+    case = DecodeCase(g["q"][:, :, 0].copy(), cache, bt, np.full(B, N, np.int32), cb, cb, R,
+                      H_kv, 16, exp)
+    out = run_gpu_decode(case, gpu, gs=4)
+    check(out, exp)
+    check(out, g["out"][:, :, 0])
+
+
+def test_decode_graph_replay(gpu):
+    """Captured decode replays match eager output on every replay."""
+    from sub0_amd.cda.kernels_cuda.wrappers import decode_hmma_v1
+    case = make_decode_case(91, [777, 1500, 64], H_kv=8, gs=4)
+    dev = gpu
+    q = torch.from_numpy(case.q.copy()).to(dev)
+    cache = torch.from_numpy(case.cache).to(dev)
+    bt = torch.from_numpy(case.block_table).to(dev)
+    sl = torch.from_numpy(case.seq_lens).to(dev)
+    cb = torch.from_numpy(case.cb_k).to(dev)
+    R = torch.from_numpy(case.R).to(dev)
+    out = torch.empty_like(q)
+
+    def call():
+        decode_hmma_v1(q, cache, bt, sl, out, cb_K=cb, cb_V=cb, rotation_fp32=R,
+                       rotation_fp16=R.half(), group_size=4, block_size=16, max_seq_len=1500)
+
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for _ in range(3):
+            call()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    eager = out.clone()
+    check(eager.cpu().numpy(), case.expected)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        call()
+    for _ in range(3):
+        out.fill_(float("nan"))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager)

@@ -1,0 +1,87 @@
+"""GPU fused paged encode: bit-exact against the CPU checker (through the C ABI)."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import cda_oracle as O
+from oracle import synth
+
+pytestmark = pytest.mark.gpu
+
+
+def expected_cache(k, v, slots, cb, num_slots, slot_bytes, sentinel):
+    T, H_kv, _ = k.shape
+    kp, kn, _ = O.encode(k, cb)
+    vp, vn, _ = O.encode(v, cb)
+    kb = kp.shape[-1]
+    cache = np.full((num_slots, H_kv, slot_bytes), sentinel, dtype=np.uint8)
+    for t in range(T):
+        s = slots[t]
+        if s < 0:
+            continue
+        cache[s, :, :kb] = kp[t]
+        cache[s, :, kb:2 * kb] = vp[t]
+        cache[s, :, 2 * kb:2 * kb + 4] = kn[t].astype(np.float32).view(np.uint8).reshape(H_kv, 4)
+        cache[s, :, 2 * kb + 4:2 * kb + 8] = vn[t].astype(np.float32).view(np.uint8).reshape(H_kv, 4)
+    return cache
+
+
+def run_gpu_encode(dev, k, v, slots, cb, num_slots, slot_bytes, sentinel):
+    from sub0_amd import _native
+    cache = torch.full((num_slots, k.shape[1], slot_bytes), sentinel, dtype=torch.uint8,
+                       device=dev)
+    cbt = torch.from_numpy(cb).to(dev)
+    _native.paged_encode(torch.from_numpy(k).to(dev), torch.from_numpy(v).to(dev),
+                         torch.from_numpy(slots.astype(np.int32)).to(dev), cache, cbt, cbt)
+    torch.cuda.synchronize()
+    return cache.cpu().numpy()
+
+
+@pytest.mark.parametrize("levels,slot_bytes", [(16, 144), (4, 80), (16, 160)])
+def test_encode_bit_exact(gpu, codebooks, levels, slot_bytes):
+    print(f"[encode] levels={levels} slot_bytes={slot_bytes}", flush=True)
+    cb = codebooks["lloyd_beta16" if levels == 16 else "lloyd_beta4"]
+    T, H_kv = 300, 8
+    k = synth.kv_with_outliers(501, (T, H_kv, 128))
+    v = synth.normal_f16(502, (T, H_kv, 128))
+    num_slots = 512
+    slots = synth.permuted_block_table(503, 1, num_slots)[0][:T].astype(np.int64)
+    slots[::17] = -1                      # padding tokens are skipped
+    exp = expected_cache(k, v, slots, cb, num_slots, slot_bytes, 0xA5)
+    got = run_gpu_encode(gpu, k, v, slots, cb, num_slots, slot_bytes, 0xA5)
+    bad = np.argwhere(got != exp)
+    assert bad.size == 0, f"{len(bad)} mismatching bytes, first {bad[:5].tolist()}"
+
+
+def test_encode_golden_rows(gpu, golden, codebooks):
+    """The fixture rows (outliers + edge rows) through the GPU encoder: equal to
+    the checker bit for bit, and equal to the reference's indices."""
+    e = golden("encode.npz")
+    x = e["x"]                            # (rows, 128)
+    rows = x.shape[0]
+    for levels, tag in ((16, "k4"), (4, "k2")):
+        cb = codebooks["lloyd_beta16" if levels == 16 else "lloyd_beta4"]
+        kb = 64 if levels == 16 else 32
+        sb = 144 if levels == 16 else 80
+        xx = x.reshape(rows, 1, 128)
+        got = run_gpu_encode(gpu, xx, xx, np.arange(rows), cb, rows, sb, 0)
+        kp, kn, _ = O.encode(x, cb)
+        assert np.array_equal(got[:, 0, :kb], kp)
+        gn = got[:, 0, 2 * kb:2 * kb + 4].copy().view(np.float32)[:, 0]
+        assert np.array_equal(gn.view(np.uint32), kn.view(np.uint32))
+        assert np.array_equal(got[:, 0, :kb], e[f"{tag}_idx"])
+
+
+def test_encode_config2_scale(gpu, codebooks):
+    """Config 2: 64 sequences x U[1,256] new tokens scattered into a paged cache."""
+    cb = codebooks["lloyd_beta16"]
+    rng_lens = (synth._splitmix64(7, 64) % np.uint64(256) + np.uint64(1)).astype(np.int64)
+    T = int(rng_lens.sum())
+    H_kv = 8
+    k = synth.kv_with_outliers(601, (T, H_kv, 128))
+    v = synth.normal_f16(602, (T, H_kv, 128))
+    num_slots = 64 * 256
+    slots = synth.permuted_block_table(603, 1, num_slots)[0][:T].astype(np.int64)
+    exp = expected_cache(k, v, slots, cb, num_slots, 144, 0)
+    got = run_gpu_encode(gpu, k, v, slots, cb, num_slots, 144, 0)
+    assert np.array_equal(got, exp)
