@@ -1,0 +1,75 @@
+"""The C ABI library (CPU-side checks: loads, exports every declared symbol,
+validates arguments before touching a device)."""
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+
+
+def declared_symbols():
+    text = (ROOT / "include" / "cda_hip.h").read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(cda_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    from sub0_amd import _native
+    L = _native.lib()
+    syms = declared_symbols()
+    assert len(syms) >= 7
+    for s in syms:
+        assert hasattr(L, s), s
+    assert sorted(_native.SYMBOLS) == syms
+
+
+def test_version_and_plan():
+    from sub0_amd import _native
+    assert _native.lib().cda_hip_version() >= 100
+    tile, splits = _native.decode_plan(32, 32, 8, 65536)
+    assert tile % 32 == 0 and tile * splits >= 65536 and splits <= 512
+    tile, splits = _native.decode_plan(1, 32, 8, 4096, 100)
+    assert tile == 128 and splits == 32
+    assert _native.decode_plan(1, 32, 8, 0) == (32, 1)
+    ws1 = _native.decode_workspace_size(4, 32, 8, 4096)
+    ws2 = _native.decode_workspace_size(4, 32, 8, 65536)
+    assert 0 < ws1 <= ws2 and ws1 % 256 == 0
+
+
+def test_invalid_arguments_are_rejected_before_launch():
+    from sub0_amd import _native
+    L = _native.lib()
+    P = ctypes.c_void_p
+    dummy = P(256)
+    rc = L.cda_decode_full_hmma_v3(dummy, dummy, 16, 144, 8, dummy, 1, dummy, dummy, dummy, 16,
+                                   dummy, None, dummy, 1, 32, 3, 16, 0, 16, 0.1, dummy, 1 << 20,
+                                   None)
+    assert rc == -1 and b"group_size" in L.cda_hip_last_error()
+    rc = L.cda_decode_full_hmma_v3(dummy, dummy, 16, 144, 8, dummy, 1, dummy, dummy, dummy, 16,
+                                   dummy, None, dummy, 1, 32, 4, 8, 0, 16, 0.1, dummy, 1 << 20,
+                                   None)
+    assert rc == -1 and b"block_size" in L.cda_hip_last_error()
+    rc = L.cda_decode_full_hmma_v3(dummy, dummy, 16, 144, 8, dummy, 1, dummy, dummy, dummy, 16,
+                                   dummy, None, dummy, 1, 32, 4, 16, 0, 16, 0.1, P(512), 16, None)
+    assert rc == -3
+    rc = L.cda_paged_encode_fused(dummy, dummy, 1024, 1024, dummy, 4, dummy, 16, 144, 8, dummy,
+                                  dummy, 5, None)
+    assert rc == -1 and b"levels" in L.cda_hip_last_error()
+    rc = L.cda_paged_encode_fused(dummy, dummy, 1024, 1024, dummy, 4, dummy, 16, 72, 8, dummy,
+                                  dummy, 16, None)
+    assert rc == -1 and b"slot_bytes" in L.cda_hip_last_error()
+    assert L.cda_paged_encode_fused(None, None, 0, 0, None, 0, None, 0, 0, 0, None, None, 16,
+                                    None) == 0          # zero tokens: nothing to do
+    assert L.cda_decode_set_timing_events(dummy, None) == -1
+
+
+def test_python_binding_refuses_cpu_tensors():
+    import torch
+    from sub0_amd import _native
+    x = torch.zeros(4, 8, 128, dtype=torch.float16)
+    with pytest.raises(ValueError, match="GPU"):
+        _native.paged_encode(x, x, torch.zeros(4, dtype=torch.int32),
+                             torch.zeros(4, 8, 144, dtype=torch.uint8),
+                             torch.zeros(16), torch.zeros(16))

@@ -1,0 +1,60 @@
+"""The drop-in Python surface (cda._prebuilt_loader, cda.kernels_cuda.*),
+host-side behaviour only."""
+import pytest
+import torch
+
+
+def test_alias_makes_reference_imports_work():
+    import sub0_amd
+    sub0_amd.install_cda_alias()
+    import cda._prebuilt_loader as pl                      # noqa: F401
+    from cda.kernels_cuda.wrappers import decode_hmma_v1, paged_encode_fused_cuda  # noqa: F401
+    from cda.kernels_cuda.hmma_loader import load_decode_hmma
+    assert callable(load_decode_hmma)
+    from cda.algorithm.compression import Compressor
+    assert Compressor(128).codebook.numel() == 16
+
+
+def test_loader_names_and_errors():
+    from sub0_amd.cda._prebuilt_loader import PrebuiltMissing, load_pybind_module
+    from sub0_amd.cda.kernels_cuda import hmma_loader as H
+    m = load_pybind_module("_v1_decode_hmma_k4v4_gs4")
+    assert callable(m.cda_decode_full_hmma_v3)
+    assert load_pybind_module("_v1_decode_hmma_k4v4_gs4") is m        # cached
+    assert callable(H.load_paged_encode_fused().cda_paged_encode_fused)
+    assert H.load_decode_hmma(group_size=8) is load_pybind_module("_v1_decode_hmma_k4v4_gs8")
+    with pytest.raises(ValueError):
+        H.load_decode_hmma(group_size=2)
+    with pytest.raises(PrebuiltMissing):
+        H.load_kv_cache_update()
+    with pytest.raises(PrebuiltMissing):
+        load_pybind_module("no_such_kernel")
+    assert issubclass(PrebuiltMissing, ImportError)
+
+
+def test_wrapper_type_checks_match_reference():
+    from sub0_amd.cda.kernels_cuda.wrappers import paged_encode_fused_cuda, decode_hmma_v1
+    k = torch.zeros(2, 8, 128)
+    with pytest.raises(TypeError):
+        paged_encode_fused_cuda(k, k, torch.zeros(2, dtype=torch.int32),
+                                torch.zeros(4, 8, 144, dtype=torch.uint8),
+                                cb_K=torch.zeros(16), cb_V=torch.zeros(16))
+    k16 = torch.zeros(2, 8, 64, dtype=torch.float16)
+    with pytest.raises(ValueError):
+        paged_encode_fused_cuda(k16, k16, torch.zeros(2, dtype=torch.int32),
+                                torch.zeros(4, 8, 144, dtype=torch.uint8),
+                                cb_K=torch.zeros(16), cb_V=torch.zeros(16))
+    q = torch.zeros(1, 32, 128, dtype=torch.float16)
+    with pytest.raises(ValueError, match="fp16 output"):
+        decode_hmma_v1(q, torch.zeros(16, 8, 144, dtype=torch.uint8),
+                       torch.zeros(1, 1, dtype=torch.int32), torch.ones(1, dtype=torch.int32),
+                       torch.zeros(1, 32, 128), cb_K=torch.zeros(16), cb_V=torch.zeros(16),
+                       rotation_fp32=torch.eye(128), rotation_fp16=torch.eye(128).half(),
+                       group_size=4, block_size=16, max_seq_len=1)
+
+
+def test_choose_tile_n_policy():
+    from sub0_amd.cda.kernels_cuda.wrappers import _choose_tile_n
+    for B, N in ((1, 4096), (4, 65536), (32, 65536), (32, 1)):
+        t = _choose_tile_n(N, B=B, H_q=32)
+        assert t % 32 == 0 and t >= 32 and -(-N // t) <= 512
