@@ -46,7 +46,7 @@ def log(*a):
 
 # --------------------------------------------------------------- workload --
 
-def make_workload(B: int, N: int, dev, seed: int | None = None):
+def make_workload(B: int, N: int, dev, seed: int | None = None, identity_bt: bool = False):
     """Paged K4V4 cache of B sequences x N tokens, encoded on the GPU by the
     fused encoder from K, V ~ N(0,1) fp16 (K with 4 seeded outlier channels
     x8), plus q ~ N(0,1); synthetic data."""
@@ -58,7 +58,8 @@ def make_workload(B: int, N: int, dev, seed: int | None = None):
     cpu = torch.Generator().manual_seed(seed)
     gpu = torch.Generator(device=dev).manual_seed(seed)
     nb = (N + BS - 1) // BS
-    bt = torch.randperm(B * nb, generator=cpu).to(torch.int32).view(B, nb).to(dev)
+    perm = torch.arange(B * nb) if identity_bt else torch.randperm(B * nb, generator=cpu)
+    bt = perm.to(torch.int32).view(B, nb).to(dev)
     outl = torch.randperm(D, generator=cpu)[:4].to(dev)
     cache = torch.zeros(B * nb * BS, H_KV, 144, dtype=torch.uint8, device=dev)
     cb = lloyd_max_centroids_beta(16, D).to(dev)
@@ -80,8 +81,18 @@ def make_workload(B: int, N: int, dev, seed: int | None = None):
                 out=torch.empty_like(q), B=B, N=N)
 
 
-def decode_call(w):
+def decode_call(w, tile_n: int = 0):
     from sub0_amd.cda.kernels_cuda.wrappers import decode_hmma_v1
+
+    if tile_n > 0:       # explicit split size (tuning runs): the raw module entry
+        from sub0_amd.cda.kernels_cuda.hmma_loader import load_decode_hmma
+        mod = load_decode_hmma(group_size=H_Q // H_KV)
+
+        def call():
+            mod.cda_decode_full_hmma_v3(w["q"], w["cache"], w["bt"], w["seq"], w["cb"], w["cb"],
+                                        w["R"], w["R16"], w["out"], H_Q // H_KV, BS, tile_n,
+                                        w["N"], 1.0 / D ** 0.5)
+        return call
 
     def call():
         decode_hmma_v1(w["q"], w["cache"], w["bt"], w["seq"], w["out"], cb_K=w["cb"],
@@ -214,6 +225,10 @@ def main(argv=None):
     ap.add_argument("--N", type=int, default=65536)
     ap.add_argument("--sweep", action="store_true")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--tile-n", type=int, default=0,
+                    help="tokens per split-K partition (0 = the library's plan)")
+    ap.add_argument("--identity-block-table", action="store_true",
+                    help="contiguous pages instead of a permuted block table (diagnostic)")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="BYTES",
                     help="only run a plain device-to-device copy of BYTES (calibrates the "
                          "rocprofv3 FETCH_SIZE / WRITE_SIZE counters) and exit")
@@ -239,8 +254,8 @@ def main(argv=None):
     _native.lib()
     B, N = args.B, args.N
 
-    w = make_workload(B, N, dev)
-    fn = decode_call(w)
+    w = make_workload(B, N, dev, identity_bt=args.identity_block_table)
+    fn = decode_call(w, args.tile_n)
     g = capture(fn, args.warmup)
     for _ in range(args.warmup):
         g.replay()
@@ -256,7 +271,7 @@ def main(argv=None):
     nbytes = _native.decode_algorithmic_bytes(B, N)
     value = nbytes / (ms_per_step * 1e-3) / 1e9
     achieved = nbytes / (k_us * 1e-6) / 1e9
-    tile, splits = _native.decode_plan(B, H_Q, H_KV, N)
+    tile, splits = _native.decode_plan(B, H_Q, H_KV, N, args.tile_n)
 
     sweep = None
     if args.sweep:

@@ -13,7 +13,11 @@ from pathlib import Path
 
 import torch  # noqa: F401  -- must be loaded first so libamdhip64 resolves to torch's runtime
 
-LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libcda_hip.so"
+import os
+
+# SUB0_AMD_LIB may name another build of the same library (A/B measurements).
+LIB_PATH = Path(os.environ.get("SUB0_AMD_LIB") or
+                Path(__file__).resolve().parent / "_lib" / "libcda_hip.so")
 
 # Exported symbols (kept in sync with include/cda_hip.h; tests check both).
 SYMBOLS = (

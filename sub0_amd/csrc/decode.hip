@@ -45,6 +45,10 @@ constexpr int kChunk = 32;                // tokens per inner iteration (2 MFMA 
 constexpr int kLutDwords = 2 * 256 * 64;
 constexpr float kLog2e = 1.4426950408889634f;
 
+#ifndef CDA_DECODE_DEPTH
+#define CDA_DECODE_DEPTH 2
+#endif
+
 struct SplitParams {
     const uint16_t *q_rot;      // (B, H_q, 128) fp16
     const uint8_t *kv;          // paged cache
@@ -98,6 +102,22 @@ __device__ __forceinline__ uint32_t cvt_pk_rn(float a, float b) {
 template <int k>
 __device__ __forceinline__ uint32_t lut_addr(uint32_t w, uint32_t col) {
     return __builtin_amdgcn_perm(w, col, 0x0C020400u | ((4u + k) << 8));
+}
+
+// max / sum over the four 16-lane rows of a wave (lanes l, l^16, l^32, l^48)
+// with the gfx950 row-swap permutes; every lane gets the result.
+__device__ __forceinline__ float rows_max(float v) {
+    auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+    auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+
+__device__ __forceinline__ float rows_sum(float v) {
+    auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+    auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(b[0]) + __uint_as_float(b[1]);
 }
 
 struct Chunk {
@@ -229,44 +249,76 @@ decode_split_kernel(SplitParams p) {
         constexpr bool MASK = decltype(masked)::value;
         // ---- S = K Q^T: rows = 16 tokens of a tile, cols = GQA group.  The K
         // operand is fp16(centroid * norm), bit-identical to the reference's
-        // decoded K (compression.py:355-359).
+        // decoded K (compression.py:355-359).  All 16 table reads of a tile
+        // are issued before the first is used.
         floatx4 sc[2];
 #pragma unroll
         for (int t = 0; t < 2; ++t) {
-            floatx4 acc = {0.f, 0.f, 0.f, 0.f};
             const uint32_t w[4] = {c.kq[t].x, c.kq[t].y, c.kq[t].z, c.kq[t].w};
+            float2 cv[16];
+#pragma unroll
+            for (int s = 0; s < 4; ++s) {
+                cv[4 * s + 0] = lut2_at(lds, lut_addr<0>(w[s], colK));
+                cv[4 * s + 1] = lut2_at(lds, lut_addr<1>(w[s], colK));
+                cv[4 * s + 2] = lut2_at(lds, lut_addr<2>(w[s], colK));
+                cv[4 * s + 3] = lut2_at(lds, lut_addr<3>(w[s], colK));
+            }
             const float nk = c.nk[t];
-#define CDA_K_PAIR(K_, W_)                                                     \
-    ({                                                                         \
-        const float2 cc = lut2_at(lds, lut_addr<K_>(W_, colK));               \
-        cvt_pk_rn(cc.x * nk, cc.y * nk);                                       \
-    })
+            floatx4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int s = 0; s < 4; ++s) {
                 uint4 a;
-                a.x = CDA_K_PAIR(0, w[s]);
-                a.y = CDA_K_PAIR(1, w[s]);
-                a.z = CDA_K_PAIR(2, w[s]);
-                a.w = CDA_K_PAIR(3, w[s]);
+                a.x = cvt_pk_rn(cv[4 * s + 0].x * nk, cv[4 * s + 0].y * nk);
+                a.y = cvt_pk_rn(cv[4 * s + 1].x * nk, cv[4 * s + 1].y * nk);
+                a.z = cvt_pk_rn(cv[4 * s + 2].x * nk, cv[4 * s + 2].y * nk);
+                a.w = cvt_pk_rn(cv[4 * s + 3].x * nk, cv[4 * s + 3].y * nk);
                 acc = mfma16(a, qb[s], acc);
             }
-#undef CDA_K_PAIR
             sc[t] = acc;
         }
-        // ---- scores (log2 domain); only the last chunk of a split is masked.
-        float s2[2][4];
+        // ---- V operand: column n = r16 of tile j holds dim 8*r16 + j; k slot
+        // pairs (2p, 2p+1) = tokens (4*q4 + 2*(p%2), +1) of tile p/2.  Pair two
+        // tokens' nibbles of one dim into one byte, then one table read gives
+        // both fp16 values.  The 32 reads are issued here, ahead of the softmax.
+        uint32_t ev[4], od[4];
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int m2 = 0; m2 < 2; ++m2) {
+                const uint32_t wa = c.vw[t][2 * m2];
+                const uint32_t wb = c.vw[t][2 * m2 + 1];
+                ev[2 * t + m2] = (wa & 0xF0F0F0F0u) | ((wb >> 4) & 0x0F0F0F0Fu);
+                od[2 * t + m2] = ((wa << 4) & 0xF0F0F0F0u) | (wb & 0x0F0F0F0Fu);
+            }
+        uint4 vb[8];
+#define CDA_V_TILE(K_, SRC_, J_)                                               \
+    vb[J_].x = lut_at(lds, lut_addr<K_>(SRC_[0], colV));                       \
+    vb[J_].y = lut_at(lds, lut_addr<K_>(SRC_[1], colV));                       \
+    vb[J_].z = lut_at(lds, lut_addr<K_>(SRC_[2], colV));                       \
+    vb[J_].w = lut_at(lds, lut_addr<K_>(SRC_[3], colV));
+        CDA_V_TILE(0, ev, 0)
+        CDA_V_TILE(0, od, 1)
+        CDA_V_TILE(1, ev, 2)
+        CDA_V_TILE(1, od, 3)
+        CDA_V_TILE(2, ev, 4)
+        CDA_V_TILE(2, od, 5)
+        CDA_V_TILE(3, ev, 6)
+        CDA_V_TILE(3, od, 7)
+#undef CDA_V_TILE
+        // ---- online softmax in the log2 domain: the max is taken on the raw
+        // scores (scale > 0), the scale is fused into the exponent argument.
+        float raw[2][4];
 #pragma unroll
         for (int t = 0; t < 2; ++t)
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                s2[t][i] = sc[t][i] * p.scale_log2;
-                if (MASK && c0 + 16 * t + 4 * q4 + i >= end) s2[t][i] = -INFINITY;
+                raw[t][i] = sc[t][i];
+                if (MASK && c0 + 16 * t + 4 * q4 + i >= end) raw[t][i] = -INFINITY;
             }
-        float cmax = fmaxf(fmaxf(fmaxf(s2[0][0], s2[0][1]), fmaxf(s2[0][2], s2[0][3])),
-                           fmaxf(fmaxf(s2[1][0], s2[1][1]), fmaxf(s2[1][2], s2[1][3])));
-        cmax = fmaxf(cmax, __shfl_xor(cmax, 16));
-        cmax = fmaxf(cmax, __shfl_xor(cmax, 32));
-        const float m_new = fmaxf(m_run, cmax);
+        float cmax = fmaxf(fmaxf(fmaxf(raw[0][0], raw[0][1]), fmaxf(raw[0][2], raw[0][3])),
+                           fmaxf(fmaxf(raw[1][0], raw[1][1]), fmaxf(raw[1][2], raw[1][3])));
+        cmax = rows_max(cmax);
+        const float m_new = fmaxf(m_run, cmax * p.scale_log2);
         const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);   // m_run = -inf -> 0
         m_run = m_new;
         // ---- P (A operand of PV): row g = r16, k slot j <-> (tile j/4, token 4*q4 + j%4).
@@ -276,12 +328,12 @@ decode_split_kernel(SplitParams p) {
         for (int t = 0; t < 2; ++t)
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const float pr = __builtin_amdgcn_exp2f(s2[t][i] - m_new);
+                const float pr = __builtin_amdgcn_exp2f(fmaf(raw[t][i], p.scale_log2, -m_new));
                 psum += pr;
                 // A masked token weighs 0 (its V norm may be garbage).
                 pv[t][i] = (MASK && c0 + 16 * t + 4 * q4 + i >= end) ? 0.0f : pr * c.nv[t][i];
             }
-        l_run = l_run * alpha + psum;
+        l_run = fmaf(l_run, alpha, psum);
         uint4 pa;
         pa.x = cvt_pk_rn(pv[0][0], pv[0][1]);
         pa.y = cvt_pk_rn(pv[0][2], pv[0][3]);
@@ -309,66 +361,54 @@ decode_split_kernel(SplitParams p) {
 #pragma unroll
                 for (int i = 0; i < 4; ++i) acc_o[j][i] *= f[i];
         }
-        // ---- V operand: column n = r16 of tile j holds dim 8*r16 + j; k slot
-        // pairs (2p, 2p+1) = tokens (4*q4 + 2*(p%2), +1) of tile p/2.  Pair two
-        // tokens' nibbles of one dim into one byte, then one table read gives
-        // both fp16 values.
-        uint32_t ev[4], od[4];
 #pragma unroll
-        for (int t = 0; t < 2; ++t)
-#pragma unroll
-            for (int m2 = 0; m2 < 2; ++m2) {
-                const uint32_t wa = c.vw[t][2 * m2];
-                const uint32_t wb = c.vw[t][2 * m2 + 1];
-                ev[2 * t + m2] = (wa & 0xF0F0F0F0u) | ((wb >> 4) & 0x0F0F0F0Fu);
-                od[2 * t + m2] = ((wa << 4) & 0xF0F0F0F0u) | (wb & 0x0F0F0F0Fu);
-            }
-#define CDA_PV_TILE(K_, SRC_, J_)                                              \
-    {                                                                          \
-        uint4 vb;                                                              \
-        vb.x = lut_at(lds, lut_addr<K_>(SRC_[0], colV));                      \
-        vb.y = lut_at(lds, lut_addr<K_>(SRC_[1], colV));                      \
-        vb.z = lut_at(lds, lut_addr<K_>(SRC_[2], colV));                      \
-        vb.w = lut_at(lds, lut_addr<K_>(SRC_[3], colV));                      \
-        acc_o[J_] = mfma16(pa, vb, acc_o[J_]);                                 \
-    }
-        CDA_PV_TILE(0, ev, 0)
-        CDA_PV_TILE(0, od, 1)
-        CDA_PV_TILE(1, ev, 2)
-        CDA_PV_TILE(1, od, 3)
-        CDA_PV_TILE(2, ev, 4)
-        CDA_PV_TILE(2, od, 5)
-        CDA_PV_TILE(3, ev, 6)
-        CDA_PV_TILE(3, od, 7)
-#undef CDA_PV_TILE
+        for (int j = 0; j < 8; ++j) acc_o[j] = mfma16(pa, vb[j], acc_o[j]);
     };
 
-
-    // ---- main loop: three rotating buffers, loads run two chunks ahead; the
-    // chunk that reaches `end` is the only masked one.
+    // ---- main loop over the full 32-token chunks; loads run one chunk
+    // ahead (CDA_DECODE_DEPTH 2) or two (3).  A partial last chunk is handled
+    // after the loop, so the loop body carries no masking.
+    const int nfull = (end - start) / kChunk;
+    int i = 0;
+#if CDA_DECODE_DEPTH == 3
     Chunk ca, cb, cc;
-    int c0 = start;
-    load_chunk(ca, c0);
-    if (c0 + kChunk < end) load_chunk(cb, c0 + kChunk);
+    if (nfull > 0) load_chunk(ca, start);
+    if (nfull > 1) load_chunk(cb, start + kChunk);
 #define CDA_STEP(CUR, NEXT2)                                                   \
     {                                                                          \
-        if (c0 + 2 * kChunk < end) load_chunk(NEXT2, c0 + 2 * kChunk);         \
-        if (c0 + kChunk <= end) compute_chunk(CUR, c0, std::false_type{});              \
-        else compute_chunk(CUR, c0, std::true_type{});                                   \
-        c0 += kChunk;                                                          \
-        if (c0 >= end) break;                                                  \
+        if (i >= nfull) break;                                                 \
+        if (i + 2 < nfull) load_chunk(NEXT2, start + (i + 2) * kChunk);        \
+        compute_chunk(CUR, start + i * kChunk, std::false_type{});             \
+        ++i;                                                                   \
     }
     while (true) {
         CDA_STEP(ca, cc)
         CDA_STEP(cb, ca)
         CDA_STEP(cc, cb)
     }
+#else
+    Chunk ca, cb;
+    if (nfull > 0) load_chunk(ca, start);
+#define CDA_STEP(CUR, NEXT)                                                    \
+    {                                                                          \
+        if (i >= nfull) break;                                                 \
+        if (i + 1 < nfull) load_chunk(NEXT, start + (i + 1) * kChunk);         \
+        compute_chunk(CUR, start + i * kChunk, std::false_type{});             \
+        ++i;                                                                   \
+    }
+    while (true) {
+        CDA_STEP(ca, cb)
+        CDA_STEP(cb, ca)
+    }
+#endif
 #undef CDA_STEP
+    if (start + nfull * kChunk < end) {
+        load_chunk(ca, start + nfull * kChunk);
+        compute_chunk(ca, start + nfull * kChunk, std::true_type{});
+    }
 
     // ---- partials.
-    float l = l_run;
-    l += __shfl_xor(l, 16);
-    l += __shfl_xor(l, 32);
+    const float l = rows_sum(l_run);
     if (q4 == 0 && r16 < GS) {
         p.part_ml[(part_row + r16) * 2 + 0] = m_run;
         p.part_ml[(part_row + r16) * 2 + 1] = l;
