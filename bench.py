@@ -227,6 +227,8 @@ def main(argv=None):
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--tile-n", type=int, default=0,
                     help="tokens per split-K partition (0 = the library's plan)")
+    ap.add_argument("--general-kernel", action="store_true",
+                    help="forbid the page-streaming split kernel (A/B diagnostic)")
     ap.add_argument("--identity-block-table", action="store_true",
                     help="contiguous pages instead of a permuted block table (diagnostic)")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="BYTES",
@@ -252,6 +254,8 @@ def main(argv=None):
         return 0
     from sub0_amd import _native
     _native.lib()
+    if args.general_kernel:
+        _native.set_stream_kernel(False)
     B, N = args.B, args.N
 
     w = make_workload(B, N, dev, identity_bt=args.identity_block_table)

@@ -81,6 +81,14 @@ int cda_decode_full_hmma_v3(const void *q, const void *kv_cache, int64_t num_slo
  * NULL to stop. */
 int cda_decode_set_timing_events(void *start_event, void *stop_event);
 
+/* Selects the decode split kernel for later calls (process-wide; default 1).
+ * enable=1 lets cda_decode_full_hmma_v3 use the page-streaming kernel when the
+ * cache is 8 KV heads x 144-byte slots and cb_k == cb_v (same pointer);
+ * enable=0 always takes the general kernel.  Both produce the same result to
+ * fp32 rounding of the softmax sums.  No reference counterpart: the reference
+ * has one decode kernel; this exists for A/B measurement and tests. */
+int cda_decode_set_stream_kernel(int enable);
+
 /* ---------------------------------------------------------------- encode --
  * Replaces the reference pybind function
  *   cda_paged_encode_fused(K, V, slot_mapping, flat_cache, cb_K, cb_V)

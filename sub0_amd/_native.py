@@ -27,6 +27,7 @@ SYMBOLS = (
     "cda_decode_workspace_size",
     "cda_decode_full_hmma_v3",
     "cda_decode_set_timing_events",
+    "cda_decode_set_stream_kernel",
     "cda_paged_encode_fused",
 )
 
@@ -77,6 +78,8 @@ def lib():
             _I32, _I32, _I32, _I32, _I32, _I32, _F32, _P, _SZ, _P]
         L.cda_decode_set_timing_events.restype = _I32
         L.cda_decode_set_timing_events.argtypes = [_P, _P]
+        L.cda_decode_set_stream_kernel.restype = _I32
+        L.cda_decode_set_stream_kernel.argtypes = [_I32]
         L.cda_paged_encode_fused.restype = _I32
         L.cda_paged_encode_fused.argtypes = [
             _P, _P, _I64, _I64, _P, _I64, _P, _I64, _I32, _I32, _P, _P, _I32, _P]
@@ -181,6 +184,12 @@ def set_split_timing_events(start=None, stop=None) -> None:
     sp = None if start is None else ctypes.c_void_p(start.cuda_event)
     ep = None if stop is None else ctypes.c_void_p(stop.cuda_event)
     _check(lib().cda_decode_set_timing_events(sp, ep), "cda_decode_set_timing_events")
+
+
+def set_stream_kernel(enable: bool) -> None:
+    """Allow (default) or forbid the page-streaming decode kernel for later
+    calls in this process; forbidding it always runs the general kernel."""
+    _check(lib().cda_decode_set_stream_kernel(int(bool(enable))), "cda_decode_set_stream_kernel")
 
 
 def decode_algorithmic_bytes(B: int, N: int, H_q: int = 32, H_kv: int = 8,

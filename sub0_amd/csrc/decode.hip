@@ -424,6 +424,387 @@ decode_split_kernel(SplitParams p) {
     }
 }
 
+// ---------------------------------------------------------------------------
+// Page-streaming variant for the common cache shape: 8 KV heads x 144-byte
+// slots, a block size that is a multiple of 16 and one codebook for K and V.
+//
+// Wave h (one per KV head) streams its head's share of each 16-token page
+// (16 x 144 B = 2304 B) into a private 5-page LDS ring with the gfx950
+// direct-to-LDS DMA (buffer_load_dwordx4 ... lds): three instructions per page
+// (K codes, V codes, norms), each lane fetching one 16-byte piece.  The waves
+// never wait for each other: each one waits on its own DMA counter only, reads
+// a chunk of two pages into registers, refills the two slots at once and
+// computes while three pages are in flight (more in flight measured slower).  Within a page the pieces are laid
+// out so that every read below is free of LDS bank conflicts:
+//   [0, 1024)     K codes: piece 16*c + t = token t, 16-byte column c (0..3)
+//   [1024, 2048)  V codes: token t's 64 bytes at 64 * vslot(t)
+//   [2048, 2304)  norms:   token t's (Kn, Vn, pad) at 16 * t
+// One dequant table serves K and V: row e (256 B) holds (cb[e >> 4],
+// cb[e & 15]) in fp32 for 32 lane columns, read with one ds_read_b64 per code
+// byte; K is rebuilt as fp16(centroid * norm), V rounds the centroid to fp16.
+// ---------------------------------------------------------------------------
+
+constexpr int kStreamRowBytes = 8 * 144;
+constexpr int kPageBytes = 16 * kStreamRowBytes;          // one 16-token page, all heads
+constexpr int kHeadPage = 16 * 144;                        // one head's share: 2304 B
+constexpr int kRingPages = 3;
+constexpr int kLut2Bytes = 256 * 64 * 4;                   // 64 KiB
+constexpr int kStreamMaxPages = 1024;                      // page rows staged in LDS
+constexpr int kRingOff = kLut2Bytes;
+constexpr int kStreamPidOff = kRingOff + kWaves * kRingPages * kHeadPage;
+constexpr int kStreamLds = kStreamPidOff + kStreamMaxPages * 4;   // 161792 B
+
+typedef unsigned v4u32 __attribute__((ext_vector_type(4)));
+
+// One 16-byte-per-lane direct-to-LDS load: lane l's 16 bytes at rsrc+voff go
+// to LDS address lds_base + 16*l.  Issued through asm so the compiler does not
+// track these asynchronous LDS writes (its tracking is conservative and would
+// serialise the ring); completion is ordered by the explicit vmcnt waits.
+__device__ __forceinline__ void dma_page_chunk(v4u32 rsrc, uint32_t voff, uint32_t lds_base) {
+    asm volatile("s_mov_b32 m0, %2\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds"
+                 :: "v"(voff), "s"(rsrc), "s"(lds_base) : "memory");
+}
+
+__device__ __forceinline__ uint32_t lds_u32addr(const void *p) {
+    return (uint32_t)(size_t)(const __attribute__((address_space(3))) void *)p;
+}
+
+__device__ __forceinline__ uint32_t lds_b32(const uint8_t *base, uint32_t off) {
+    return *reinterpret_cast<const uint32_t *>(base + off);
+}
+
+// 64-byte V slot of token t within its group of four: the four tokens read
+// together (4*q4 + i, q4 = 0..3) land in four different bank quarters.
+__host__ __device__ constexpr int vslot(int t) { return (t & 12) | ((t + (t >> 2)) & 3); }
+__host__ __device__ constexpr int vslot_inv(int s) { return (s & 12) | ((s - (s >> 2)) & 3); }
+
+template <int GS>
+__global__ void __launch_bounds__(kThreads, 1)
+decode_stream_kernel(SplitParams p) {
+    __shared__ __align__(16) uint8_t smem[kStreamLds];
+
+    const int sp = blockIdx.x;
+    const int b = blockIdx.z;
+    const int tid = threadIdx.x;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int lane = tid & 63;
+    const int h = wave;                       // this variant has exactly 8 KV heads
+    const int r16 = lane & 15;
+    const int q4 = lane >> 4;
+
+    const int seq_len =
+        __builtin_amdgcn_readfirstlane(min(p.seq_lens[b], p.bt_stride * p.block_size));
+    const int start = sp * p.tile_n;
+    const int end = min(start + p.tile_n, seq_len);
+    const int64_t part_row = ((int64_t)b * p.n_splits + sp) * p.H_q + (int64_t)h * GS;
+    if (start >= end) {
+        if (q4 == 0 && r16 < GS) {
+            p.part_ml[(part_row + r16) * 2 + 0] = -INFINITY;
+            p.part_ml[(part_row + r16) * 2 + 1] = 0.0f;
+        }
+        for (int i = lane; i < GS * kD; i += 64) p.part_o[part_row * kD + i] = 0.0f;
+        return;
+    }
+
+    // ---- DMA sources (offsets in the head's share of a page) of this lane's
+    // piece in each of the three instructions; see the layout above.
+    uint32_t src[3];
+    src[0] = (uint32_t)((lane & 15) * kStreamRowBytes + (lane >> 4) * 16);
+    src[1] = (uint32_t)(vslot_inv(lane >> 2) * kStreamRowBytes + 64 + (lane & 3) * 16);
+    src[2] = (uint32_t)((lane & 15) * kStreamRowBytes + 128);   // lanes 0..15 only
+
+    const int bs = p.block_size;
+    const int npages = (end - start + 15) >> 4;     // <= kStreamMaxPages (host check)
+    const uint32_t ring_w =
+        __builtin_amdgcn_readfirstlane(lds_u32addr(smem)) + kRingOff + wave * (kRingPages * kHeadPage);
+    // First cache row of each page of the split, staged in LDS: a block-table
+    // read per page would stall the wave on memory latency before each DMA.
+    int32_t *page_row = reinterpret_cast<int32_t *>(smem + kStreamPidOff);
+    {
+        const int32_t *bt = p.block_table + (int64_t)b * p.bt_stride;
+        for (int t = tid; t < npages; t += kThreads) {
+            const int t0 = start + 16 * t;
+            page_row[t] = bt[t0 / bs] * bs + (t0 % bs);
+        }
+    }
+    const uint8_t *kv_h = p.kv + h * 144;
+    auto issue = [&](int t) {
+        const int64_t row0 = __builtin_amdgcn_readfirstlane(page_row[t]);
+        const uint64_t base = (uint64_t)(kv_h + row0 * kStreamRowBytes);
+        const v4u32 r = {(uint32_t)base, (uint32_t)(base >> 32) & 0xFFFFu,
+                         (uint32_t)(kPageBytes - h * 144), 0x00020000u};
+        const uint32_t sb = ring_w + (uint32_t)(t % kRingPages) * kHeadPage;
+        dma_page_chunk(r, src[0], sb);
+        dma_page_chunk(r, src[1], sb + 1024);
+        if (lane < 16) dma_page_chunk(r, src[2], sb + 2048);
+    };
+    // ---- query operand (B of QK^T): column g = r16, k slots = dims 32*q4+8*s+j.
+    // Columns g >= GS repeat query g % GS: their scores are never used (no
+    // alpha, m or output is read from them) and stay finite.
+    uint4 qb[4];
+    {
+        const uint16_t *qg =
+            p.q_rot + ((int64_t)b * p.H_q + (int64_t)h * GS + (r16 & (GS - 1))) * kD + 32 * q4;
+#pragma unroll
+        for (int s = 0; s < 4; ++s) qb[s] = *reinterpret_cast<const uint4 *>(qg + 8 * s);
+    }
+
+    // ---- dequant table.
+    {
+        uint32_t *lut = reinterpret_cast<uint32_t *>(smem);
+        for (int i = tid; i < kLut2Bytes / 4; i += kThreads) {
+            const int e = i >> 6;
+            lut[i] = __float_as_uint(p.cb_k[(i & 1) ? (e & 15) : (e >> 4)]);
+        }
+    }
+    __syncthreads();
+    // Every vector load the compiler issued above has landed: from here on the
+    // vector-memory counter tracks this wave's DMAs only.
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+
+    // Ring prologue: pages 0..2 (as many as exist).  Page t lives in slot t % 3.
+#pragma unroll
+    for (int t = 0; t < kRingPages; ++t)
+        if (t < npages) issue(t);
+
+    // Per-lane read offsets inside a page share.
+    // Per-lane read offsets inside this wave's ring (slot 0); the slot adds
+    // a compile-time immediate.
+    const uint32_t rb0 = (uint32_t)(kRingOff + wave * (kRingPages * kHeadPage));
+    const uint32_t oK = rb0 + (uint32_t)lane * 16u;
+    const uint32_t oNK = rb0 + 2048u + 16u * r16;
+    uint32_t oV[4], oNV[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        oV[i] = rb0 + 1024u + 64u * vslot(4 * q4 + i) + 4u * r16;
+        oNV[i] = rb0 + 2048u + 16u * (4 * q4 + i) + 4u;
+    }
+    const uint32_t col = (uint32_t)(lane & 31) * 8u;
+    const uint8_t *lutb = smem;
+
+    floatx4 acc_o[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc_o[j] = floatx4{0.f, 0.f, 0.f, 0.f};
+    float m_run = -INFINITY;
+    float l_run = 0.0f;
+
+    // (cb[hi], cb[lo]) of code byte k of w: one 8-byte read.
+#define CDA_PAIR(K_, W_) (*reinterpret_cast<const float2 *>(lutb + lut_addr<K_>(W_, col)))
+
+    struct PageRegs {
+        uint4 kq;          // K codes: token r16, dims [32*q4, 32*q4+32)
+        float nk;          // K norm of token r16
+        uint32_t vw[4];    // V codes: token 4*q4+k, dims [8*r16, 8*r16+8)
+        float nv[4];       // V norm of token 4*q4+k
+    };
+    auto read_page = [&](PageRegs &r, auto slot) {
+        constexpr uint32_t so = decltype(slot)::value * kHeadPage;
+        r.kq = *reinterpret_cast<const uint4 *>(smem + oK + so);
+        r.nk = __uint_as_float(lds_b32(smem + so, oNK));
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            r.vw[k] = lds_b32(smem + so, oV[k]);
+            r.nv[k] = __uint_as_float(lds_b32(smem + so, oNV[k]));
+        }
+    };
+
+    // ---- scores of one page: its 16 tokens (rows) x the queries (columns).
+    auto page_scores = [&](const PageRegs &r) -> floatx4 {
+        const uint32_t w[4] = {r.kq.x, r.kq.y, r.kq.z, r.kq.w};
+        float2 cv[16];
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            cv[4 * s + 0] = CDA_PAIR(0, w[s]);
+            cv[4 * s + 1] = CDA_PAIR(1, w[s]);
+            cv[4 * s + 2] = CDA_PAIR(2, w[s]);
+            cv[4 * s + 3] = CDA_PAIR(3, w[s]);
+        }
+        const float nk = r.nk;
+        floatx4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            uint4 a;
+            a.x = cvt_pk_rn(cv[4 * s + 0].x * nk, cv[4 * s + 0].y * nk);
+            a.y = cvt_pk_rn(cv[4 * s + 1].x * nk, cv[4 * s + 1].y * nk);
+            a.z = cvt_pk_rn(cv[4 * s + 2].x * nk, cv[4 * s + 2].y * nk);
+            a.w = cvt_pk_rn(cv[4 * s + 3].x * nk, cv[4 * s + 3].y * nk);
+            acc = mfma16(a, qb[s], acc);
+        }
+        return acc;
+    };
+
+    // ---- softmax + PV over a chunk of two pages; tokens at or past `end`
+    // weigh 0.
+    auto finish_chunk = [&](floatx4 sc0, floatx4 sc1, const PageRegs &r0, const PageRegs &r1,
+                            int c0, auto masked) {
+        constexpr bool MASK = decltype(masked)::value;
+        // V operand (B of PV): column r16 of tile j holds dim 8*r16 + j; k slot
+        // pairs (2p, 2p+1) = tokens (4*q4 + 2*(p%2), +1) of page p/2.  Pair two
+        // tokens' nibbles of one dim into one byte, so one table read gives
+        // both values.
+        uint32_t ev[4], od[4];
+#pragma unroll
+        for (int m2 = 0; m2 < 2; ++m2) {
+            ev[m2] = (r0.vw[2 * m2] & 0xF0F0F0F0u) | ((r0.vw[2 * m2 + 1] >> 4) & 0x0F0F0F0Fu);
+            od[m2] = ((r0.vw[2 * m2] << 4) & 0xF0F0F0F0u) | (r0.vw[2 * m2 + 1] & 0x0F0F0F0Fu);
+            ev[2 + m2] = (r1.vw[2 * m2] & 0xF0F0F0F0u) | ((r1.vw[2 * m2 + 1] >> 4) & 0x0F0F0F0Fu);
+            od[2 + m2] = ((r1.vw[2 * m2] << 4) & 0xF0F0F0F0u) | (r1.vw[2 * m2 + 1] & 0x0F0F0F0Fu);
+        }
+        float2 vc[32];
+#define CDA_V_TILE(K_, SRC_, J_)                                               \
+    vc[4 * (J_) + 0] = CDA_PAIR(K_, SRC_[0]);                                  \
+    vc[4 * (J_) + 1] = CDA_PAIR(K_, SRC_[1]);                                  \
+    vc[4 * (J_) + 2] = CDA_PAIR(K_, SRC_[2]);                                  \
+    vc[4 * (J_) + 3] = CDA_PAIR(K_, SRC_[3]);
+        CDA_V_TILE(0, ev, 0)
+        CDA_V_TILE(0, od, 1)
+        CDA_V_TILE(1, ev, 2)
+        CDA_V_TILE(1, od, 3)
+        CDA_V_TILE(2, ev, 4)
+        CDA_V_TILE(2, od, 5)
+        CDA_V_TILE(3, ev, 6)
+        CDA_V_TILE(3, od, 7)
+#undef CDA_V_TILE
+        float raw[2][4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            raw[0][i] = sc0[i];
+            raw[1][i] = sc1[i];
+            if (MASK && c0 + 4 * q4 + i >= end) raw[0][i] = -INFINITY;
+            if (MASK && c0 + 16 + 4 * q4 + i >= end) raw[1][i] = -INFINITY;
+        }
+        float cmax = fmaxf(fmaxf(fmaxf(raw[0][0], raw[0][1]), fmaxf(raw[0][2], raw[0][3])),
+                           fmaxf(fmaxf(raw[1][0], raw[1][1]), fmaxf(raw[1][2], raw[1][3])));
+        cmax = rows_max(cmax);
+        const float m_new = fmaxf(m_run, cmax * p.scale_log2);
+        const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);   // m_run = -inf -> 0
+        m_run = m_new;
+        float pv[2][4];
+        float psum = 0.0f;
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float pr = __builtin_amdgcn_exp2f(fmaf(raw[t][i], p.scale_log2, -m_new));
+                psum += pr;
+                // A masked token weighs 0 (its ring slot may hold stale data).
+                const float nvv = t ? r1.nv[i] : r0.nv[i];
+                pv[t][i] = (MASK && c0 + 16 * t + 4 * q4 + i >= end) ? 0.0f : pr * nvv;
+            }
+        l_run = fmaf(l_run, alpha, psum);
+        uint4 pa;
+        pa.x = cvt_pk_rn(pv[0][0], pv[0][1]);
+        pa.y = cvt_pk_rn(pv[0][2], pv[0][3]);
+        pa.z = cvt_pk_rn(pv[1][0], pv[1][1]);
+        pa.w = cvt_pk_rn(pv[1][2], pv[1][3]);
+        float al[GS];
+        bool moved = false;
+#pragma unroll
+        for (int g = 0; g < GS; ++g) {
+            al[g] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(alpha), g));
+            moved |= (al[g] != 1.0f);
+        }
+        if (moved) {
+            float f[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                f[i] = 1.0f;
+#pragma unroll
+                for (int g = 0; g < GS; ++g)
+                    if (4 * q4 + i == g) f[i] = al[g];
+            }
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) acc_o[j][i] *= f[i];
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            uint4 vb;
+            vb.x = cvt_pk_rn(vc[4 * j + 0].x, vc[4 * j + 0].y);
+            vb.y = cvt_pk_rn(vc[4 * j + 1].x, vc[4 * j + 1].y);
+            vb.z = cvt_pk_rn(vc[4 * j + 2].x, vc[4 * j + 2].y);
+            vb.w = cvt_pk_rn(vc[4 * j + 3].x, vc[4 * j + 3].y);
+            acc_o[j] = mfma16(pa, vb, acc_o[j]);
+        }
+    };
+#undef CDA_PAIR
+
+    // ---- main loop over chunks of two pages.  Chunk i: wait for this wave's
+    // DMAs of pages <= 2i+1, read both pages into registers, refill their
+    // slots with pages 2i+5, 2i+6, then compute.
+    auto step = [&](int i, auto sa, auto sb, auto masked) {
+        // DMAs allowed in flight = 3 per page issued beyond page 2i+1 (<= 3
+        // pages); vmcnt takes an immediate, hence the case split.
+        const int ahead = max(min(npages, 2 * i + kRingPages) - (2 * i + 2), 0);
+        switch (ahead) {
+        case 3: __builtin_amdgcn_s_waitcnt(0x0F70 | 9); break;
+        case 2: __builtin_amdgcn_s_waitcnt(0x0F70 | 6); break;
+        case 1: __builtin_amdgcn_s_waitcnt(0x0F70 | 3); break;
+        default: __builtin_amdgcn_s_waitcnt(0x0F70); break;
+        }
+        asm volatile("" ::: "memory");
+        PageRegs r0, r1;
+        read_page(r0, sa);
+        if (2 * i + 1 < npages) {
+            read_page(r1, sb);
+        } else {
+            // A chunk of one page: the second half is past `end`, masked out.
+            r1.kq = make_uint4(0, 0, 0, 0);
+            r1.nk = 0.0f;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                r1.vw[k] = 0u;
+                r1.nv[k] = 0.0f;
+            }
+        }
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        if (2 * i + kRingPages < npages) issue(2 * i + kRingPages);
+        if (2 * i + kRingPages + 1 < npages) issue(2 * i + kRingPages + 1);
+        const floatx4 sc0 = page_scores(r0);
+        const floatx4 sc1 = page_scores(r1);
+        finish_chunk(sc0, sc1, r0, r1, start + 32 * i, masked);
+    };
+    // Full chunks first (no masking in the loop body), then the partial one.
+    // Chunk i reads slots (2i) % 3 and (2i+1) % 3: the slot pattern repeats
+    // every three chunks, so the loop is unrolled by three.
+    using S0 = std::integral_constant<int, 0>;
+    using S1 = std::integral_constant<int, 1>;
+    using S2 = std::integral_constant<int, 2>;
+    const int nchunks = (npages + 1) >> 1;
+    const int nfull = (end - start) >> 5;
+    int i = 0;
+    for (; i + 3 <= nfull; i += 3) {
+        step(i, S0{}, S1{}, std::false_type{});
+        step(i + 1, S2{}, S0{}, std::false_type{});
+        step(i + 2, S1{}, S2{}, std::false_type{});
+    }
+    for (; i < nfull; ++i) {
+        if (i % 3 == 0) step(i, S0{}, S1{}, std::false_type{});
+        else step(i, S2{}, S0{}, std::false_type{});      // i % 3 == 1 (at most two left)
+    }
+    if (nfull < nchunks) {
+        if (nfull % 3 == 0) step(nfull, S0{}, S1{}, std::true_type{});
+        else if (nfull % 3 == 1) step(nfull, S2{}, S0{}, std::true_type{});
+        else step(nfull, S1{}, S2{}, std::true_type{});
+    }
+
+    const float l = rows_sum(l_run);
+    if (q4 == 0 && r16 < GS) {
+        p.part_ml[(part_row + r16) * 2 + 0] = m_run;
+        p.part_ml[(part_row + r16) * 2 + 1] = l;
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int g = 4 * q4 + i;
+        if (g < GS) {
+            float4 *dst = reinterpret_cast<float4 *>(p.part_o + (part_row + g) * kD + 8 * r16);
+            dst[0] = make_float4(acc_o[0][i], acc_o[1][i], acc_o[2][i], acc_o[3][i]);
+            dst[1] = make_float4(acc_o[4][i], acc_o[5][i], acc_o[6][i], acc_o[7][i]);
+        }
+    }
+}
+
 // q_rot[b, h, j] = fp16(sum_k fp32(q[b, h, k]) * R[k, j]).  The blocks also
 // share the transpose of R (one column per block per pass) for the epilogue.
 __global__ void __launch_bounds__(128)
@@ -530,6 +911,8 @@ WsLayout ws_layout(int B, int H_q, int n_splits) {
 // Optional profiling events recorded around the split kernel (per thread).
 thread_local hipEvent_t g_split_start = nullptr;
 thread_local hipEvent_t g_split_stop = nullptr;
+// Lets tests run the general kernel on shapes the streaming kernel also covers.
+bool g_allow_stream = true;
 
 int num_cus() {
     static int cached = 0;
@@ -651,12 +1034,23 @@ extern "C" int cda_decode_full_hmma_v3(const void *q, const void *kv_cache, int6
     p.n_splits = ns;
     p.scale_log2 = scale * kLog2e;
     dim3 grid(ns, (H_kv + kWaves - 1) / kWaves, B);
+    // The page-streaming kernel covers 8 KV heads x 144-byte slots with one
+    // codebook for K and V (passed as the same pointer) and splits of at most
+    // 1024 pages; anything else takes the general kernel.
+    const bool use_stream = H_kv == 8 && slot_bytes == kStreamRowBytes / 8 && cb_k == cb_v &&
+                            tn <= 16 * kStreamMaxPages && g_allow_stream;
     if (g_split_start && hipEventRecord(g_split_start, st) != hipSuccess)
         return fail(CDA_E_HIP, "cda_decode_full_hmma_v3: hipEventRecord(start) failed");
-    if (group_size == 4)
+    if (use_stream) {
+        if (group_size == 4)
+            decode_stream_kernel<4><<<grid, kThreads, 0, st>>>(p);
+        else
+            decode_stream_kernel<8><<<grid, kThreads, 0, st>>>(p);
+    } else if (group_size == 4) {
         decode_split_kernel<4><<<grid, kThreads, 0, st>>>(p);
-    else
+    } else {
         decode_split_kernel<8><<<grid, kThreads, 0, st>>>(p);
+    }
     CDA_LAUNCH_CHECK("decode_split_kernel");
     if (g_split_stop && hipEventRecord(g_split_stop, st) != hipSuccess)
         return fail(CDA_E_HIP, "cda_decode_full_hmma_v3: hipEventRecord(stop) failed");
@@ -672,5 +1066,10 @@ extern "C" int cda_decode_set_timing_events(void *start_event, void *stop_event)
                 "cda_decode_set_timing_events: pass both events or neither");
     g_split_start = static_cast<hipEvent_t>(start_event);
     g_split_stop = static_cast<hipEvent_t>(stop_event);
+    return CDA_OK;
+}
+
+extern "C" int cda_decode_set_stream_kernel(int enable) {
+    g_allow_stream = enable != 0;
     return CDA_OK;
 }

@@ -64,6 +64,30 @@ def test_decode_matches_checker(gpu, name, seq_lens, H_kv, gs, bs, tile_n, fill)
     check(out, case.expected)
 
 
+@pytest.mark.parametrize("name,seq_lens,gs,bs,tile_n", [
+    ("cfg0_shape", [4096], 4, 16, 0),
+    ("ragged", [33, 1000, 17, 2049], 4, 16, 0),
+    ("gs8", [500, 1500], 8, 16, 0),
+    ("block32_tile64", [999, 64], 4, 32, 64),
+])
+def test_decode_general_kernel_matches_checker(gpu, name, seq_lens, gs, bs, tile_n):
+    """The same 8-head, 144-byte-slot cases with the page-streaming kernel
+    forbidden: the general kernel must meet the same bar, and both kernels
+    must agree with each other."""
+    from sub0_amd import _native
+    print(f"[decode-general] case={name} seq_lens={seq_lens} gs={gs} bs={bs}", flush=True)
+    case = make_decode_case(2000 + len(name), seq_lens, H_kv=8, gs=gs, block_size=bs, fill=0xFF)
+    streamed = run_gpu_decode(case, gpu, gs=gs, tile_n=tile_n)
+    _native.set_stream_kernel(False)
+    try:
+        general = run_gpu_decode(case, gpu, gs=gs, tile_n=tile_n)
+    finally:
+        _native.set_stream_kernel(True)
+    check(general, case.expected)
+    check(streamed, case.expected)
+    check(streamed, general, tol=1e-3)
+
+
 def test_decode_scale_and_slack_max_seq_len(gpu):
     """Non-default softmax scale; max_seq_len larger than every seq_len."""
     case = make_decode_case(77, [400, 250], H_kv=8, gs=4, scale=0.3)
