@@ -203,14 +203,14 @@ def cpu_baseline(threads: int | None = None, reps: int = 3):
 
 # -------------------------------------------------------------------- main --
 
-def load_traffic(B, N):
-    """HBM bytes per split-kernel launch from the committed rocprofv3 PMC summary."""
-    p = ROOT / "profiles" / "decode_split_traffic.json"
+def load_traffic(kernel, B, N):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 PMC summary."""
+    p = ROOT / "profiles" / "decode_traffic.json"
     if not p.is_file():
         return None
     try:
         d = json.loads(p.read_text())
-        cell = d.get("cells", {}).get(f"{B},{N}")
+        cell = d.get("kernels", {}).get(kernel, {}).get(f"{B},{N}")
         return None if cell is None else int(cell["hbm_bytes_per_launch"])
     except (ValueError, KeyError, TypeError):
         return None
@@ -312,7 +312,10 @@ def main(argv=None):
         except Exception as e:  # the baseline is reported, never required
             log(f"cpu baseline skipped: {e!r}")
 
-    traffic = load_traffic(B, N)
+    # The workload (8 KV heads, 144-byte slots, one codebook) is eligible for
+    # the page-streaming kernel unless it is switched off.
+    kernel = "decode_split_kernel" if args.general_kernel else "decode_stream_kernel"
+    traffic = load_traffic(kernel, B, N)
     line = {
         "metric": METRIC,
         "value": round(value, 1),
@@ -336,7 +339,7 @@ def main(argv=None):
                    "tile_n": tile, "splits": splits, "algorithmic_bytes": nbytes},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / PEAK_GBS, 4),
-                     "traffic": traffic, "kernel": "decode_split_kernel",
+                     "traffic": traffic, "kernel": kernel,
                      "kernel_us": round(k_us, 2)},
         "cpu_baseline": cpu,
     }

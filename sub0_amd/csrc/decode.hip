@@ -805,22 +805,38 @@ decode_stream_kernel(SplitParams p) {
     }
 }
 
-// q_rot[b, h, j] = fp16(sum_k fp32(q[b, h, k]) * R[k, j]).  The blocks also
-// share the transpose of R (one column per block per pass) for the epilogue.
-__global__ void __launch_bounds__(128)
-rotate_q_kernel(const uint16_t *q, const float *R, uint16_t *q_rot, float *RT, int H_q) {
-    __shared__ float qs[kD];
-    const int h = blockIdx.x, b = blockIdx.y, j = threadIdx.x;
-    const int64_t row = ((int64_t)b * H_q + h) * kD;
-    qs[j] = h2f(q[row + j]);
-    const int nblk = gridDim.x * gridDim.y;
-    for (int c = blockIdx.y * gridDim.x + blockIdx.x; c < kD; c += nblk)
-        RT[c * kD + j] = R[j * kD + c];
+// q_rot[b, h, j] = fp16(sum_k fp32(q[b, h, k]) * R[k, j]).  One 256-thread
+// block per (4 q-heads, sequence): R is staged in LDS once (all its loads in
+// flight together), then wave w computes head w, two output columns per lane.
+constexpr int kHeadsPerBlock = 4;
+
+__global__ void __launch_bounds__(256)
+rotate_q_kernel(const uint16_t *q, const float *R, uint16_t *q_rot, int H_q) {
+    __shared__ __align__(16) float Rs[kD * kD];
+    __shared__ float qs[kHeadsPerBlock][kD];
+    const int b = blockIdx.y, t = threadIdx.x;
+    const int h0 = blockIdx.x * kHeadsPerBlock;
+    const float4 *R4 = reinterpret_cast<const float4 *>(R);
+    float4 *Rs4 = reinterpret_cast<float4 *>(Rs);
+#pragma unroll
+    for (int i = 0; i < kD * kD / 4 / 256; ++i) Rs4[t + 256 * i] = R4[t + 256 * i];
+    for (int i = t; i < kHeadsPerBlock * kD; i += 256) {
+        const int hh = i / kD, k = i % kD;
+        qs[hh][k] = (h0 + hh < H_q) ? h2f(q[((int64_t)b * H_q + h0 + hh) * kD + k]) : 0.0f;
+    }
     __syncthreads();
-    float acc = 0.0f;
+    const int hh = t >> 6, j = 2 * (t & 63);
+    if (h0 + hh >= H_q) return;
+    float a0 = 0.0f, a1 = 0.0f;
 #pragma unroll 8
-    for (int k = 0; k < kD; ++k) acc = fmaf(qs[k], R[k * kD + j], acc);
-    q_rot[row + j] = __half_as_ushort(__float2half_rn(acc));
+    for (int k = 0; k < kD; ++k) {
+        const float2 r = *reinterpret_cast<const float2 *>(Rs + k * kD + j);
+        a0 = fmaf(qs[hh][k], r.x, a0);
+        a1 = fmaf(qs[hh][k], r.y, a1);
+    }
+    const int64_t row = ((int64_t)b * H_q + h0 + hh) * kD;
+    q_rot[row + j] = __half_as_ushort(__float2half_rn(a0));
+    q_rot[row + j + 1] = __half_as_ushort(__float2half_rn(a1));
 }
 
 constexpr int kMaxSplits = 1024;
@@ -839,58 +855,91 @@ __device__ __forceinline__ float wave_sum(float v) {
 
 // Merge split partials (attention.py:239-272: m* = max m_i, weights
 // exp(m_i - m*), empty splits weigh 0, l clamped at 1e-30), round O_rot to
-// fp16 and unrotate with R^T.  One 128-thread block per (q-head, sequence);
-// the split loop is spread over the threads.
-__global__ void __launch_bounds__(128)
-combine_kernel(const float *part_o, const float *part_ml, const float *RT, uint16_t *out,
+// fp16 and unrotate with R^T.  One 256-thread block per (4 q-heads,
+// sequence): wave w merges head w (two dims per lane, 16 splits' loads in
+// flight at a time); R^T is staged in LDS for the epilogue.
+__global__ void __launch_bounds__(256)
+combine_kernel(const float *part_o, const float *part_ml, const float *R, uint16_t *out,
                int H_q, int n_splits) {
-    __shared__ float orot[kD];
-    __shared__ float wts[kMaxSplits];
-    __shared__ float red[2];
-    const int h = blockIdx.x, b = blockIdx.y, j = threadIdx.x;
-    const int wave = j >> 6;
+    __shared__ __align__(16) float RT[kD * kD];
+    __shared__ float wts[kHeadsPerBlock][kMaxSplits];
+    __shared__ float orot[kHeadsPerBlock][kD];
+    const int b = blockIdx.y, t = threadIdx.x;
+    const int h0 = blockIdx.x * kHeadsPerBlock;
+    const int hh = t >> 6, lane = t & 63;
+    const int h = h0 + hh;
+    // R^T into LDS: lane-consecutive j on each write, so the writes do not
+    // conflict; the reads below are row reads of RT.
+    for (int i = t; i < kD * kD / 4; i += 256) {
+        const int j = i % kD, k4 = (i / kD) * 4;
+        const float4 r = *reinterpret_cast<const float4 *>(R + j * kD + k4);
+        RT[(k4 + 0) * kD + j] = r.x;
+        RT[(k4 + 1) * kD + j] = r.y;
+        RT[(k4 + 2) * kD + j] = r.z;
+        RT[(k4 + 3) * kD + j] = r.w;
+    }
+    const bool live = h < H_q;
     const int64_t base = (int64_t)b * n_splits * H_q + h;
-    float mx = -INFINITY;
-    for (int s = j; s < n_splits; s += kD) mx = fmaxf(mx, part_ml[(base + (int64_t)s * H_q) * 2]);
-    mx = wave_max(mx);
-    if ((j & 63) == 0) red[wave] = mx;
-    __syncthreads();
-    mx = fmaxf(red[0], red[1]);
-    __syncthreads();
-    float lp = 0.0f;
-    for (int s = j; s < n_splits; s += kD) {
-        const int64_t r = base + (int64_t)s * H_q;
-        const float ms = part_ml[r * 2];
-        const float w = (ms == -INFINITY) ? 0.0f : exp2f(ms - mx);
-        wts[s] = w;
-        if (w != 0.0f) lp += w * part_ml[r * 2 + 1];
+    float L = 0.0f;
+    if (live) {
+        float mx = -INFINITY;
+        for (int s = lane; s < n_splits; s += 64)
+            mx = fmaxf(mx, part_ml[(base + (int64_t)s * H_q) * 2]);
+        mx = wave_max(mx);
+        float lp = 0.0f;
+        for (int s = lane; s < n_splits; s += 64) {
+            const int64_t r = base + (int64_t)s * H_q;
+            const float ms = part_ml[r * 2];
+            const float w = (ms == -INFINITY) ? 0.0f : exp2f(ms - mx);
+            wts[hh][s] = w;
+            if (w != 0.0f) lp += w * part_ml[r * 2 + 1];
+        }
+        L = wave_sum(lp);
     }
-    lp = wave_sum(lp);
-    if ((j & 63) == 0) red[wave] = lp;
     __syncthreads();
-    const float L = red[0] + red[1];
-    // Empty splits store zeros, so every partial can be read unconditionally
-    // (which lets the loads run ahead of the FMAs).
-    float o[4] = {0.f, 0.f, 0.f, 0.f};
-    const float *po = part_o + base * kD + j;
-    const int64_t step = (int64_t)H_q * kD;
-    int s = 0;
-    for (; s + 3 < n_splits; s += 4) {
+    if (live) {
+        // Empty splits store zeros, so every partial is read unconditionally.
+        const float *po = part_o + base * kD + 2 * lane;
+        const int64_t step = (int64_t)H_q * kD;
+        float o0 = 0.0f, o1 = 0.0f;
+        int s = 0;
+        for (; s + 16 <= n_splits; s += 16) {
+            float2 v[16];
 #pragma unroll
-        for (int u = 0; u < 4; ++u) o[u] += wts[s + u] * po[(int64_t)(s + u) * step];
+            for (int u = 0; u < 16; ++u)
+                v[u] = *reinterpret_cast<const float2 *>(po + (int64_t)(s + u) * step);
+#pragma unroll
+            for (int u = 0; u < 16; ++u) {
+                o0 = fmaf(wts[hh][s + u], v[u].x, o0);
+                o1 = fmaf(wts[hh][s + u], v[u].y, o1);
+            }
+        }
+        for (; s < n_splits; ++s) {
+            const float2 v = *reinterpret_cast<const float2 *>(po + (int64_t)s * step);
+            o0 = fmaf(wts[hh][s], v.x, o0);
+            o1 = fmaf(wts[hh][s], v.y, o1);
+        }
+        const float inv = 1.0f / fmaxf(L, 1e-30f);
+        orot[hh][2 * lane] = h2f(__half_as_ushort(__float2half_rn(o0 * inv)));
+        orot[hh][2 * lane + 1] = h2f(__half_as_ushort(__float2half_rn(o1 * inv)));
     }
-    for (; s < n_splits; ++s) o[0] += wts[s] * po[(int64_t)s * step];
-    const float v = ((o[0] + o[1]) + (o[2] + o[3])) / fmaxf(L, 1e-30f);
-    orot[j] = h2f(__half_as_ushort(__float2half_rn(v)));
     __syncthreads();
-    float acc = 0.0f;
+    if (!live) return;
+    const int j = 2 * lane;
+    float a0 = 0.0f, a1 = 0.0f;
 #pragma unroll 8
-    for (int k = 0; k < kD; ++k) acc = fmaf(orot[k], RT[k * kD + j], acc);
-    out[((int64_t)b * H_q + h) * kD + j] = __half_as_ushort(__float2half_rn(acc));
+    for (int k = 0; k < kD; ++k) {
+        const float2 r = *reinterpret_cast<const float2 *>(RT + k * kD + j);
+        a0 = fmaf(orot[hh][k], r.x, a0);
+        a1 = fmaf(orot[hh][k], r.y, a1);
+    }
+    const int64_t row = ((int64_t)b * H_q + h) * kD;
+    out[row + j] = __half_as_ushort(__float2half_rn(a0));
+    out[row + j + 1] = __half_as_ushort(__float2half_rn(a1));
 }
 
 struct WsLayout {
-    size_t q_rot, rt, part_o, part_ml, total;
+    size_t q_rot, part_o, part_ml, total;
 };
 
 WsLayout ws_layout(int B, int H_q, int n_splits) {
@@ -898,8 +947,6 @@ WsLayout ws_layout(int B, int H_q, int n_splits) {
     size_t off = 0;
     w.q_rot = off;
     off += align256((size_t)B * H_q * kD * 2);
-    w.rt = off;
-    off += align256((size_t)kD * kD * 4);
     w.part_o = off;
     off += align256((size_t)B * n_splits * H_q * kD * 4);
     w.part_ml = off;
@@ -1010,9 +1057,9 @@ extern "C" int cda_decode_full_hmma_v3(const void *q, const void *kv_cache, int6
     hipStream_t st = static_cast<hipStream_t>(stream);
 
     uint16_t *q_rot = reinterpret_cast<uint16_t *>(ws + w.q_rot);
-    float *RT = reinterpret_cast<float *>(ws + w.rt);
-    rotate_q_kernel<<<dim3(H_q, B), 128, 0, st>>>(static_cast<const uint16_t *>(q), rot_f32,
-                                                   q_rot, RT, H_q);
+    const dim3 head_grid((H_q + kHeadsPerBlock - 1) / kHeadsPerBlock, B);
+    rotate_q_kernel<<<head_grid, 256, 0, st>>>(static_cast<const uint16_t *>(q), rot_f32, q_rot,
+                                               H_q);
     CDA_LAUNCH_CHECK("rotate_q_kernel");
 
     SplitParams p;
@@ -1055,7 +1102,7 @@ extern "C" int cda_decode_full_hmma_v3(const void *q, const void *kv_cache, int6
     if (g_split_stop && hipEventRecord(g_split_stop, st) != hipSuccess)
         return fail(CDA_E_HIP, "cda_decode_full_hmma_v3: hipEventRecord(stop) failed");
 
-    combine_kernel<<<dim3(H_q, B), 128, 0, st>>>(p.part_o, p.part_ml, RT,
+    combine_kernel<<<head_grid, 256, 0, st>>>(p.part_o, p.part_ml, rot_f32,
                                                  static_cast<uint16_t *>(out), H_q, ns);
     CDA_LAUNCH_CHECK("combine_kernel");
     return CDA_OK;

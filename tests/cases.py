@@ -26,7 +26,7 @@ class DecodeCase:
 
 
 def make_decode_case(seed, seq_lens, *, H_kv=8, gs=4, block_size=16, cb=None, extra_blocks=3,
-                     scale=None, fill=0):
+                     scale=None, fill=0, cb_v=None):
     """Encode seeded K/V per sequence with the checker, scatter into a paged
     cache through a permuted block table, and compute the checker's output."""
     seq_lens = np.asarray(seq_lens, dtype=np.int32)
@@ -34,6 +34,8 @@ def make_decode_case(seed, seq_lens, *, H_kv=8, gs=4, block_size=16, cb=None, ex
     H_q = H_kv * gs
     if cb is None:
         cb = synth_cb()
+    if cb_v is None:
+        cb_v = cb
     nmax = max(1, int(seq_lens.max()))
     W = (nmax + block_size - 1) // block_size + extra_blocks
     bt = synth.permuted_block_table(seed, B, W)
@@ -41,13 +43,13 @@ def make_decode_case(seed, seq_lens, *, H_kv=8, gs=4, block_size=16, cb=None, ex
     v = synth.normal_f16(seed + 1, (B, H_kv, nmax, D))
     q = synth.normal_f16(seed + 2, (B, H_q, D))
     kp, kn, _ = O.encode(k, cb)
-    vp, vn, _ = O.encode(v, cb)
+    vp, vn, _ = O.encode(v, cb_v)
     cache = O.build_paged_cache(kp, kn, vp, vn, bt, block_size, cb.size,
                                 num_blocks=B * W, fill=fill)
     R = O.hadamard128()
-    exp = O.decode_paged(q, cache, bt, seq_lens, cb, cb, R, H_kv=H_kv,
+    exp = O.decode_paged(q, cache, bt, seq_lens, cb, cb_v, R, H_kv=H_kv,
                          block_size=block_size, scale=scale)
-    return DecodeCase(q, cache, bt, seq_lens, cb, cb, R, H_kv, block_size, exp)
+    return DecodeCase(q, cache, bt, seq_lens, cb, cb_v, R, H_kv, block_size, exp)
 
 
 _CB = None

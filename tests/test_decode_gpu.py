@@ -16,17 +16,18 @@ pytestmark = pytest.mark.gpu
 TOL = 2e-3
 
 
-def run_gpu_decode(case, dev, *, gs, tile_n=0, max_seq_len=None, scale=None):
+def run_gpu_decode(case, dev, *, gs, tile_n=0, max_seq_len=None, scale=None, cb_copy=False):
     from sub0_amd import _native
     q = torch.from_numpy(case.q.copy()).to(dev)
     cache = torch.from_numpy(case.cache).to(dev)
     bt = torch.from_numpy(case.block_table).to(dev)
     sl = torch.from_numpy(case.seq_lens).to(dev)
     cb = torch.from_numpy(case.cb_k).to(dev)
+    cbv = cb if (case.cb_v is case.cb_k and not cb_copy) else torch.from_numpy(case.cb_v.copy()).to(dev)
     R = torch.from_numpy(case.R).to(dev)
     out = torch.full_like(q, float("nan"))
     msl = int(case.seq_lens.max()) if max_seq_len is None else max_seq_len
-    _native.decode(q, cache, bt, sl, cb, cb, R, R.half(), out, group_size=gs,
+    _native.decode(q, cache, bt, sl, cb, cbv, R, R.half(), out, group_size=gs,
                    block_size=case.block_size, tile_n=tile_n, max_seq_len=msl,
                    scale=scale if scale is not None else 1.0 / np.sqrt(128))
     torch.cuda.synchronize()
@@ -88,6 +89,22 @@ def test_decode_general_kernel_matches_checker(gpu, name, seq_lens, gs, bs, tile
     check(streamed, general, tol=1e-3)
 
 
+def test_decode_separate_equal_codebooks(gpu):
+    """cb_K and cb_V as separate tensors with equal values (the reference
+    passes one Compressor's codebook each)."""
+    case = make_decode_case(3001, [700, 1300], H_kv=8, gs=4, fill=0xFF)
+    out = run_gpu_decode(case, gpu, gs=4, cb_copy=True)
+    check(out, case.expected)
+
+
+def test_decode_different_v_codebook(gpu):
+    """V encoded with its own codebook (uniform 16 levels): K and V tables differ."""
+    cbv = O.uniform_centroids(16)
+    case = make_decode_case(3002, [900, 33], H_kv=8, gs=4, cb_v=cbv, fill=0xFF)
+    out = run_gpu_decode(case, gpu, gs=4)
+    check(out, case.expected)
+
+
 def test_decode_scale_and_slack_max_seq_len(gpu):
     """Non-default softmax scale; max_seq_len larger than every seq_len."""
     case = make_decode_case(77, [400, 250], H_kv=8, gs=4, scale=0.3)
@@ -132,11 +149,12 @@ def test_decode_graph_replay(gpu):
     bt = torch.from_numpy(case.block_table).to(dev)
     sl = torch.from_numpy(case.seq_lens).to(dev)
     cb = torch.from_numpy(case.cb_k).to(dev)
+    cbv = cb.clone()        # separate tensors with equal values, as the reference passes them
     R = torch.from_numpy(case.R).to(dev)
     out = torch.empty_like(q)
 
     def call():
-        decode_hmma_v1(q, cache, bt, sl, out, cb_K=cb, cb_V=cb, rotation_fp32=R,
+        decode_hmma_v1(q, cache, bt, sl, out, cb_K=cb, cb_V=cbv, rotation_fp32=R,
                        rotation_fp16=R.half(), group_size=4, block_size=16, max_seq_len=1500)
 
     s = torch.cuda.Stream()
