@@ -109,6 +109,60 @@ int cda_paged_encode_fused(const void *k, const void *v, int64_t k_stride, int64
                            int64_t num_slots, int slot_bytes, int H_kv, const float *cb_k,
                            const float *cb_v, int levels, void *stream);
 
+/* --------------------------------------------------------------- prefill --
+ * Causal varlen prefill with the Hadamard-128 rotation of Q fused in front and
+ * the inverse rotation of O fused behind (bottom-right causal alignment:
+ * key k is visible to query i of sequence b iff k <= i + seq_k[b] - seq_q[b]).
+ * O_rot is rounded to fp16 before the inverse rotation (attention.py:93).
+ *
+ * cda_prefill_paged_hadamard reads K/V straight from the compressed K4V4
+ * paged cache (tiles are dequantised into LDS, no dense scratch).  It replaces
+ * the pair paged_cache_to_dense_rotated + cda_fa2_varlen_fwd_hadamard that
+ * fa2_cda_prefill_varlen_v1(fuse_fa2_epilogue=True) runs
+ * (cda/kernels_cuda/fa2_cda.py:98-230).  No single reference symbol.
+ *   q, out:        (T, H_q, 128) fp16, unrotated; T = cu_seqlens_q[B].
+ *   cu_seqlens_q:  (B+1,) int32.   seq_lens: (B,) int32 key lengths.
+ *   H_q / H_kv:    4 or 8.         levels: 16.
+ */
+int cda_prefill_paged_hadamard(const void *q, const void *kv_cache, int64_t num_slots,
+                               int slot_bytes, int H_kv, const int32_t *block_table,
+                               int bt_stride, const int32_t *cu_seqlens_q,
+                               const int32_t *seq_lens, int B, const float *cb_k,
+                               const float *cb_v, int levels, void *out, int T, int H_q,
+                               int block_size, int max_query_len, float scale, void *stream);
+
+/* Replaces the reference pybind function
+ *   cda_fa2_varlen_fwd_hadamard(Q, k_rot, v_rot, out, cu_q, cu_k, seqused_k,
+ *                               max_q, max_k, scale)      (causal only)
+ * bound by cda/kernels_cuda/fa2_cda.py:166-181 (module _v1_fa2_cda_varlen_fused,
+ * hmma_loader.py:56-58).  k_rot, v_rot: dense rotated fp16 rows
+ * (rows, H_kv, 128); sequence b's keys are rows cu_seqlens_k[b] ..
+ * cu_seqlens_k[b] + seqused_k[b] - 1. */
+int cda_fa2_varlen_fwd_hadamard(const void *q, const void *k_rot, const void *v_rot, void *out,
+                                const int32_t *cu_seqlens_q, const int32_t *cu_seqlens_k,
+                                const int32_t *seqused_k, int B, int T, int H_q, int H_kv,
+                                int max_query_len, int max_seq_len, float scale, void *stream);
+
+/* Replaces the reference pybind function
+ *   cda_fa2_paged_cache_to_dense_rotated(kv, block_table, seq_lens, cb_K, cb_V,
+ *                                        block_size, max_seq_len) -> (k_rot, v_rot)
+ * bound by cda/kernels_cuda/fa2_cda.py:85-95 (module _v1_fa2_cda_loader_k4v4,
+ * hmma_loader.py:45-48).  Writes k_out, v_out: (B * max_seq_len, H_kv, 128)
+ * fp16, row b*max_seq_len + t = fp16(centroid * norm) for t < seq_lens[b],
+ * zeros beyond.  K4V4 only. */
+int cda_fa2_paged_cache_to_dense_rotated(const void *kv_cache, int64_t num_slots, int slot_bytes,
+                                         int H_kv, const int32_t *block_table, int bt_stride,
+                                         const int32_t *seq_lens, int B, const float *cb_k,
+                                         const float *cb_v, int levels, int block_size,
+                                         int max_seq_len, void *k_out, void *v_out,
+                                         void *stream);
+
+/* Replaces the reference pybind function hadamard128_fp16(x, y, scale)
+ * (cda/kernels_cuda/fa2_cda.py:51-52, module _v1_fa2_cda_hadamard128):
+ * y = fp16(scale * x @ H_128) for `rows` rows of 128 fp16, H the unnormalised
+ * Sylvester matrix (natural order). */
+int cda_hadamard128_fp16(const void *x, void *y, int64_t rows, float scale, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

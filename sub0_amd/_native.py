@@ -30,6 +30,10 @@ SYMBOLS = (
     "cda_decode_set_timing_events",
     "cda_decode_set_stream_kernel",
     "cda_paged_encode_fused",
+    "cda_prefill_paged_hadamard",
+    "cda_fa2_varlen_fwd_hadamard",
+    "cda_fa2_paged_cache_to_dense_rotated",
+    "cda_hadamard128_fp16",
 )
 
 
@@ -84,6 +88,18 @@ def lib():
         L.cda_paged_encode_fused.restype = _I32
         L.cda_paged_encode_fused.argtypes = [
             _P, _P, _I64, _I64, _P, _I64, _P, _I64, _I32, _I32, _P, _P, _I32, _P]
+        L.cda_prefill_paged_hadamard.restype = _I32
+        L.cda_prefill_paged_hadamard.argtypes = [
+            _P, _P, _I64, _I32, _I32, _P, _I32, _P, _P, _I32, _P, _P, _I32, _P, _I32, _I32,
+            _I32, _I32, _F32, _P]
+        L.cda_fa2_varlen_fwd_hadamard.restype = _I32
+        L.cda_fa2_varlen_fwd_hadamard.argtypes = [
+            _P, _P, _P, _P, _P, _P, _P, _I32, _I32, _I32, _I32, _I32, _I32, _F32, _P]
+        L.cda_fa2_paged_cache_to_dense_rotated.restype = _I32
+        L.cda_fa2_paged_cache_to_dense_rotated.argtypes = [
+            _P, _I64, _I32, _I32, _P, _I32, _P, _I32, _P, _P, _I32, _I32, _I32, _P, _P, _P]
+        L.cda_hadamard128_fp16.restype = _I32
+        L.cda_hadamard128_fp16.argtypes = [_P, _P, _I64, _F32, _P]
         _lib = L
     return _lib
 
@@ -263,3 +279,104 @@ def paged_encode(k: torch.Tensor, v: torch.Tensor, slot_mapping: torch.Tensor,
         _ptr(flat_cache), flat_cache.shape[0], flat_cache.shape[2], H_kv,
         _ptr(cb_k.float().contiguous()), _ptr(cb_v.float().contiguous()), levels, _stream(dev))
     _check(rc, "cda_paged_encode_fused")
+
+
+# ----------------------------------------------------------------- prefill --
+
+def _check_paged(kv_cache, block_table, seq_lens, cb_k, cb_v):
+    if kv_cache.dtype != torch.uint8 or kv_cache.dim() != 3 or not kv_cache.is_contiguous():
+        raise ValueError("kv_cache must be a contiguous uint8 (num_slots, H_kv, slot_bytes) tensor")
+    if block_table.dtype != torch.int32 or block_table.dim() != 2 or block_table.stride(1) != 1:
+        raise ValueError("block_table must be int32 (B, max_blocks) with unit inner stride")
+    if seq_lens.dtype != torch.int32:
+        raise TypeError("seq_lens must be int32")
+    if cb_k.numel() != 16 or cb_v.numel() != 16:
+        raise ValueError("the prefill kernels read K4V4 caches (16-level codebooks)")
+
+
+def prefill_paged(q: torch.Tensor, kv_cache: torch.Tensor, block_table: torch.Tensor,
+                  cu_seqlens_q: torch.Tensor, seq_lens: torch.Tensor, cb_k: torch.Tensor,
+                  cb_v: torch.Tensor, out: torch.Tensor, *, block_size: int,
+                  max_query_len: int, scale: float) -> None:
+    """Causal varlen prefill straight from the compressed paged cache with the
+    Hadamard prologue/epilogue; ``out`` (T, H_q, 128) fp16 is written in place."""
+    dev = _require_gpu(q, kv_cache, block_table, cu_seqlens_q, seq_lens, cb_k, cb_v, out)
+    if q.dtype != torch.float16 or out.dtype != torch.float16:
+        raise TypeError("Q and output must be fp16")
+    if q.dim() != 3 or q.shape[-1] != 128 or not q.is_contiguous():
+        raise ValueError("Q must be a contiguous (T, H_q, 128) tensor")
+    if out.shape != q.shape or not out.is_contiguous():
+        raise ValueError("output must be a contiguous tensor shaped like Q")
+    if cu_seqlens_q.dtype != torch.int32:
+        raise TypeError("cu_seqlens_q must be int32")
+    _check_paged(kv_cache, block_table, seq_lens, cb_k, cb_v)
+    T, H_q, _ = q.shape
+    B = cu_seqlens_q.numel() - 1
+    if seq_lens.numel() < B or block_table.shape[0] < B:
+        raise ValueError("seq_lens / block_table have fewer rows than cu_seqlens_q")
+    num_slots, H_kv, slot_bytes = kv_cache.shape
+    rc = lib().cda_prefill_paged_hadamard(
+        _ptr(q), _ptr(kv_cache), num_slots, slot_bytes, H_kv, _ptr(block_table),
+        block_table.stride(0), _ptr(cu_seqlens_q), _ptr(seq_lens), B,
+        _ptr(cb_k.float().contiguous()), _ptr(cb_v.float().contiguous()), 16, _ptr(out), T, H_q,
+        int(block_size), int(max_query_len), float(scale), _stream(dev))
+    _check(rc, "cda_prefill_paged_hadamard")
+
+
+def fa2_varlen_fwd_hadamard(q: torch.Tensor, k_rot: torch.Tensor, v_rot: torch.Tensor,
+                            out: torch.Tensor, cu_seqlens_q: torch.Tensor,
+                            cu_seqlens_k: torch.Tensor, seqused_k: torch.Tensor,
+                            max_query_len: int, max_seq_len: int, scale: float) -> None:
+    """Causal varlen attention over dense rotated fp16 K/V rows with the
+    Hadamard prologue on Q and the inverse rotation on O (the reference's
+    cda_fa2_varlen_fwd_hadamard, fa2_cda.py:166-181)."""
+    dev = _require_gpu(q, k_rot, v_rot, out, cu_seqlens_q, cu_seqlens_k, seqused_k)
+    for t, nm in ((q, "Q"), (k_rot, "k_rot"), (v_rot, "v_rot"), (out, "output")):
+        if t.dtype != torch.float16:
+            raise TypeError(f"{nm} must be fp16")
+        if t.dim() != 3 or t.shape[-1] != 128 or not t.is_contiguous():
+            raise ValueError(f"{nm} must be a contiguous (rows, heads, 128) tensor")
+    if k_rot.shape != v_rot.shape or out.shape != q.shape:
+        raise ValueError("k_rot/v_rot and Q/output must have matching shapes")
+    for t, nm in ((cu_seqlens_q, "cu_seqlens_q"), (cu_seqlens_k, "cu_seqlens_k"),
+                  (seqused_k, "seqused_k")):
+        if t.dtype != torch.int32:
+            raise TypeError(f"{nm} must be int32")
+    T, H_q, _ = q.shape
+    B = cu_seqlens_q.numel() - 1
+    rc = lib().cda_fa2_varlen_fwd_hadamard(
+        _ptr(q), _ptr(k_rot), _ptr(v_rot), _ptr(out), _ptr(cu_seqlens_q),
+        _ptr(cu_seqlens_k), _ptr(seqused_k), B, T, H_q, k_rot.shape[1], int(max_query_len),
+        int(max_seq_len), float(scale), _stream(dev))
+    _check(rc, "cda_fa2_varlen_fwd_hadamard")
+
+
+def paged_to_dense(kv_cache: torch.Tensor, block_table: torch.Tensor, seq_lens: torch.Tensor,
+                   cb_k: torch.Tensor, cb_v: torch.Tensor, *, block_size: int,
+                   max_seq_len: int) -> tuple[torch.Tensor, torch.Tensor]:
+    """Dense rotated fp16 K/V, (B * max_seq_len, H_kv, 128) each, zero past
+    seq_lens (fa2_cda.py:64-95)."""
+    dev = _require_gpu(kv_cache, block_table, seq_lens, cb_k, cb_v)
+    _check_paged(kv_cache, block_table, seq_lens, cb_k, cb_v)
+    B = seq_lens.numel()
+    num_slots, H_kv, slot_bytes = kv_cache.shape
+    k_out = torch.empty(B * max_seq_len, H_kv, 128, dtype=torch.float16, device=dev)
+    v_out = torch.empty_like(k_out)
+    rc = lib().cda_fa2_paged_cache_to_dense_rotated(
+        _ptr(kv_cache), num_slots, slot_bytes, H_kv, _ptr(block_table), block_table.stride(0),
+        _ptr(seq_lens), B, _ptr(cb_k.float().contiguous()), _ptr(cb_v.float().contiguous()), 16,
+        int(block_size), int(max_seq_len), _ptr(k_out), _ptr(v_out), _stream(dev))
+    _check(rc, "cda_fa2_paged_cache_to_dense_rotated")
+    return k_out, v_out
+
+
+def hadamard128(x: torch.Tensor, y: torch.Tensor, scale: float) -> None:
+    """y = fp16(scale * x @ H_128) row-wise (Sylvester order); x, y fp16 with a
+    last dimension of 128."""
+    dev = _require_gpu(x, y)
+    if x.dtype != torch.float16 or y.dtype != torch.float16:
+        raise TypeError("x and y must be fp16")
+    if x.shape[-1] != 128 or x.shape != y.shape or not x.is_contiguous() or not y.is_contiguous():
+        raise ValueError("x and y must be contiguous, of one shape, last dimension 128")
+    rc = lib().cda_hadamard128_fp16(_ptr(x), _ptr(y), x.numel() // 128, float(scale), _stream(dev))
+    _check(rc, "cda_hadamard128_fp16")

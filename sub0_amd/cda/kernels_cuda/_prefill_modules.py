@@ -1,0 +1,64 @@
+"""Module objects for the prefill kernel names of the reference loader
+(``hmma_loader.py:45-58``): the paged -> dense rotated loader, the fused
+varlen forward with the Hadamard prologue/epilogue, and the Hadamard-128
+helper.  Each forwards to the MI355X C ABI through :mod:`sub0_amd._native`.
+"""
+from __future__ import annotations
+
+from types import ModuleType
+
+from sub0_amd import _native
+
+
+def _flat_cache(kv_cache):
+    if kv_cache.dim() == 4:
+        nb, bs, h, w = kv_cache.shape
+        return kv_cache.view(nb * bs, h, w)
+    return kv_cache
+
+
+def _loader_module(name: str) -> ModuleType:
+    mod = ModuleType(name)
+    mod.__doc__ = "Paged K4V4 cache -> dense rotated fp16 K/V (MI355X)."
+
+    def cda_fa2_paged_cache_to_dense_rotated(kv_cache, block_table, seq_lens, cb_K, cb_V,
+                                             block_size, max_seq_len):
+        """Positional signature of the reference call (fa2_cda.py:85-95)."""
+        return _native.paged_to_dense(_flat_cache(kv_cache), block_table, seq_lens, cb_K, cb_V,
+                                      block_size=int(block_size), max_seq_len=int(max_seq_len))
+
+    mod.cda_fa2_paged_cache_to_dense_rotated = cda_fa2_paged_cache_to_dense_rotated
+    return mod
+
+
+def _varlen_module(name: str) -> ModuleType:
+    mod = ModuleType(name)
+    mod.__doc__ = "Causal varlen attention with Hadamard prologue/epilogue (MI355X)."
+
+    def cda_fa2_varlen_fwd_hadamard(Q, k_rot, v_rot, out, cu_q, cu_k, seqused_k, max_q, max_k,
+                                    scale):
+        """Positional signature of the reference call (fa2_cda.py:166-181)."""
+        _native.fa2_varlen_fwd_hadamard(Q, k_rot, v_rot, out, cu_q, cu_k, seqused_k,
+                                        int(max_q), int(max_k), float(scale))
+
+    mod.cda_fa2_varlen_fwd_hadamard = cda_fa2_varlen_fwd_hadamard
+    return mod
+
+
+def _hadamard_module(name: str) -> ModuleType:
+    mod = ModuleType(name)
+    mod.__doc__ = "Row-wise Hadamard-128 transform of fp16 rows (MI355X)."
+
+    def hadamard128_fp16(x, y, scale):
+        """Positional signature of the reference call (fa2_cda.py:51-52)."""
+        _native.hadamard128(x, y, float(scale))
+
+    mod.hadamard128_fp16 = hadamard128_fp16
+    return mod
+
+
+FACTORIES = {
+    "_v1_fa2_cda_loader_k4v4": lambda: _loader_module("_v1_fa2_cda_loader_k4v4"),
+    "_v1_fa2_cda_varlen_fused": lambda: _varlen_module("_v1_fa2_cda_varlen_fused"),
+    "_v1_fa2_cda_hadamard128": lambda: _hadamard_module("_v1_fa2_cda_hadamard128"),
+}

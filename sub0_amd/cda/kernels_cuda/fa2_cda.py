@@ -1,0 +1,128 @@
+"""CDA prefill (drop-in for ``cda/kernels_cuda/fa2_cda.py``).
+
+Same public functions and argument handling as the reference
+(``fa2_cda.py:36-230``).  On MI355X the fused path
+(``fuse_fa2_epilogue=True``) does not materialise dense K/V in HBM: one
+kernel dequantises 64-key tiles of the compressed paged cache into LDS and
+runs a causal flash attention on MFMA with the Hadamard rotation of Q in
+front and the inverse rotation of O behind.  With ``return_dense_kv=True``
+the dense rotated K/V are materialised (the reference's stage-0 bridge) and
+the same attention runs over them.  The unfused path of the reference calls
+vLLM's FlashAttention around two Hadamard transforms; here it computes the
+same quantity (fp16 q_rot, fp16 O_rot, fp16 output) with the fused kernel.
+"""
+from __future__ import annotations
+
+import math
+from typing import Optional
+
+import torch
+from torch import Tensor
+
+from sub0_amd import _native
+from sub0_amd.cda.kernels_cuda.hmma_loader import (
+    load_fa2_cda_hadamard,
+    load_fa2_cda_loader,
+    load_fa2_cda_varlen_fused,
+)
+
+
+def _hadamard_or_matmul(x: Tensor, rotation_fp32: Tensor, *,
+                        out: Optional[Tensor] = None) -> Tensor:
+    """x @ H/sqrt(D) rounded to fp16 (fa2_cda.py:36-61): the Hadamard kernel
+    for contiguous fp16 D=128 device tensors, a matmul with ``rotation_fp32``
+    otherwise."""
+    D = x.shape[-1]
+    if (D == 128 and x.is_cuda and x.dtype == torch.float16 and x.is_contiguous()
+            and (out is None or (out.is_cuda and out.dtype == torch.float16
+                                 and out.is_contiguous()))):
+        y = torch.empty_like(x) if out is None else out
+        load_fa2_cda_hadamard().hadamard128_fp16(x, y, 1.0 / math.sqrt(D))
+        return y
+    y = torch.matmul(x.float(), rotation_fp32).to(torch.float16)
+    if out is not None:
+        out.copy_(y)
+        return out
+    return y
+
+
+def paged_cache_to_dense_rotated(kv_cache: Tensor, block_table: Tensor, seq_lens: Tensor, *,
+                                 cb_K: Tensor, cb_V: Tensor, block_size: int, max_seq_len: int,
+                                 k4v2: bool = False) -> tuple[Tensor, Tensor]:
+    """Dense rotated K/V ``(B * max_seq_len, H_kv, 128)`` fp16, zero past
+    ``seq_lens[b]`` (fa2_cda.py:64-95)."""
+    bt = block_table.to(torch.int32) if block_table.dtype != torch.int32 else block_table
+    sl = seq_lens.to(torch.int32) if seq_lens.dtype != torch.int32 else seq_lens
+    mod = load_fa2_cda_loader(k4v2=k4v2)
+    return mod.cda_fa2_paged_cache_to_dense_rotated(kv_cache, bt, sl, cb_K.contiguous(),
+                                                    cb_V.contiguous(), int(block_size),
+                                                    int(max_seq_len))
+
+
+def fa2_cda_prefill_varlen_v1(
+    Q_fp16: Tensor,           # (T, H_q, D) fp16, unrotated
+    kv_cache: Tensor,         # (num_slots, H_kv, slot_w) uint8 K4V4
+    block_table: Tensor,      # (B, max_blocks) int32
+    cu_seqlens_q: Tensor,     # (B+1,) int32
+    seq_lens: Tensor,         # (B,) int32, full key lengths
+    output: Tensor,           # (T, H_q, D) fp16, written in place
+    *,
+    cb_K: Tensor,
+    cb_V: Tensor,
+    rotation_fp32: Tensor,
+    group_size: int,
+    block_size: int,
+    max_query_len: int,
+    max_seq_len: int,
+    scale: Optional[float] = None,
+    causal: bool = True,
+    k4v2: bool = False,
+    return_dense_kv: bool = False,
+    fuse_fa2_epilogue: bool = False,
+) -> tuple[Tensor, Tensor] | None:
+    """Causal varlen prefill from the compressed cache (fa2_cda.py:98-230).
+    Queries are the last ``cu_seqlens_q[b+1] - cu_seqlens_q[b]`` positions of
+    each sequence; key k is visible to query i iff k <= i + seq_lens[b] -
+    (its query count)."""
+    if Q_fp16.dim() != 3:
+        raise ValueError("Q_fp16 must be (T, H_q, D)")
+    if output.shape != Q_fp16.shape:
+        raise ValueError("output shape must match Q_fp16")
+    if output.dtype != torch.float16:
+        raise ValueError("output must be fp16")
+    Q_in = Q_fp16 if Q_fp16.dtype == torch.float16 else Q_fp16.to(torch.float16)
+    T, H_q, D = Q_in.shape
+    B = int(cu_seqlens_q.numel()) - 1
+    if B <= 0:
+        return None
+    if H_q % group_size != 0:
+        raise ValueError("H_q must be divisible by group_size")
+    if not causal:
+        raise NotImplementedError("the MI355X prefill kernels are causal-only")
+    if k4v2:
+        load_fa2_cda_loader(k4v2=True)   # raises PrebuiltMissing: no K4V2 build
+    if scale is None:
+        scale = 1.0 / math.sqrt(D)
+    cu_q = cu_seqlens_q.to(torch.int32) if cu_seqlens_q.dtype != torch.int32 else cu_seqlens_q
+    sl = seq_lens.to(torch.int32) if seq_lens.dtype != torch.int32 else seq_lens
+    bt = block_table.to(torch.int32) if block_table.dtype != torch.int32 else block_table
+    kv = kv_cache.view(-1, *kv_cache.shape[-2:]) if kv_cache.dim() == 4 else kv_cache
+    out = output if output.is_contiguous() else torch.empty_like(output)
+    if return_dense_kv:
+        k_rot, v_rot = paged_cache_to_dense_rotated(kv, bt, sl, cb_K=cb_K, cb_V=cb_V,
+                                                    block_size=block_size,
+                                                    max_seq_len=max_seq_len)
+        cu_k = torch.arange(0, B + 1, dtype=torch.int32, device=Q_in.device) * int(max_seq_len)
+        load_fa2_cda_varlen_fused().cda_fa2_varlen_fwd_hadamard(
+            Q_in.contiguous(), k_rot, v_rot, out, cu_q.contiguous(), cu_k, sl.contiguous(),
+            int(max_query_len), int(max_seq_len), float(scale))
+    else:
+        load_fa2_cda_varlen_fused()      # same artefact family as the reference's fused path
+        _native.prefill_paged(Q_in.contiguous(), kv, bt, cu_q.contiguous(), sl.contiguous(),
+                              cb_K, cb_V, out, block_size=int(block_size),
+                              max_query_len=int(max_query_len), scale=float(scale))
+    if out is not output:
+        output.copy_(out)
+    if return_dense_kv:
+        return k_rot, v_rot
+    return None

@@ -1,0 +1,665 @@
+// Varlen causal prefill for CDA (gfx950): flash attention whose K/V tiles are
+// materialised in LDS, with the Hadamard-128 rotation of Q as a prologue and
+// the inverse rotation of O as an epilogue, both on MFMA.
+//
+// Reference contract: fa2_cda_prefill_varlen_v1 (cda/kernels_cuda/fa2_cda.py:
+// 98-230) with fuse_fa2_epilogue=True: Q is unrotated fp16, the cache holds
+// Hadamard-rotated codes, the mask is causal with bottom-right alignment
+// (k <= q + seq_k - seq_q per sequence), O_rot is rounded to fp16 before the
+// inverse rotation (attention.py:93, :482) and the output is unrotated fp16.
+// Math per (query, head): attention_reference (attention.py:60-93) on K and V
+// decoded as fp16(centroid * norm) (compression.py:355-359).
+//
+// Two K/V sources share the kernel:
+//   * Paged: the compressed K4V4 cache; each 64-token tile is dequantised by
+//     the whole workgroup straight into LDS (no dense scratch in HBM).
+//   * Dense: fp16 rotated K/V rows (the reference's cda_fa2_varlen_fwd_hadamard
+//     over the output of paged_cache_to_dense_rotated).
+//
+// Workgroup = 8 waves = the GQA group of one KV head x 32*(8/GS) queries: wave
+// w takes q-head h*GS + w % GS and 32 queries.  Per wave all products are
+// 32x32x16 f16 MFMAs laid out so that no lane ever exchanges data:
+//   q_rot^T = H q^T           (prologue; result columns = queries)
+//   S^T     = K q_rot^T       (rows = 32 keys, columns = the wave's queries)
+//   O^T    += V^T P^T         (P^T taken straight from the S^T accumulators)
+//   out^T   = H fp16(O^T / l) (epilogue)
+// The k index of each product is permuted to match the accumulator rows it is
+// fed from; the other operand (H, an LDS tile) is read in the same order.
+#include "cda_common.h"
+
+#include <cmath>
+
+namespace cda {
+namespace {
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+
+constexpr int kD = 128;
+constexpr int kBN = 64;                  // keys per tile
+constexpr int kWaves = 8;
+constexpr int kThreads = 64 * kWaves;
+constexpr float kLog2e = 1.4426950408889634f;
+
+// LDS: two tile buffers (K [64 keys][128 dims] and V^T [128 dims][64 keys],
+// fp16, 16 KiB each), then the per-code dequant tables (paged source).
+constexpr int kTileBytes = 2 * kBN * kD * 2;
+constexpr int kLutOff = 2 * kTileBytes;               // 64 KiB
+constexpr int kLutBytes = 2 * 16 * 64 * 4;             // K and V, 16 codes x 64 columns
+constexpr int kPrefillLds = kLutOff + kLutBytes;
+
+__device__ __forceinline__ floatx16 mfma32(half8 a, half8 b, floatx16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+
+// Unnormalised Sylvester Hadamard entry (+-1): H[i][j] = (-1)^popcount(i & j).
+__device__ __forceinline__ _Float16 hsign(int i, int j) {
+    return (__builtin_popcount(i & j) & 1) ? (_Float16)-1.0f : (_Float16)1.0f;
+}
+
+// Dimension carried by k slot j of k-step (T, s) in lane half u: the row of the
+// 32x32 accumulator register 8s + j of tile T.
+__device__ __forceinline__ int kdim(int T, int s, int u, int j) {
+    return 32 * T + 16 * s + 8 * (j >> 2) + 4 * u + (j & 3);
+}
+
+__device__ __forceinline__ uint32_t cvt_pk(float a, float b) {
+    typedef float f2 __attribute__((ext_vector_type(2)));
+    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f2{a, b}, h2));
+}
+
+__device__ __forceinline__ half8 pack8(const floatx16 &c, int base, float scale) {
+    const uint4 v = make_uint4(cvt_pk(c[base + 0] * scale, c[base + 1] * scale),
+                               cvt_pk(c[base + 2] * scale, c[base + 3] * scale),
+                               cvt_pk(c[base + 4] * scale, c[base + 5] * scale),
+                               cvt_pk(c[base + 6] * scale, c[base + 7] * scale));
+    return __builtin_bit_cast(half8, v);
+}
+
+// K tile: key t's 4-dim group G (8 bytes) at t*256 + 8*(G ^ (t & 31)).
+__device__ __forceinline__ uint32_t k_off(int t, int G) {
+    return (uint32_t)(t * 256 + 8 * (G ^ (t & 31)));
+}
+// V^T tile: dim d's 4-key group g at d*128 + 8*(g ^ ((d >> 1) & 15)).
+__device__ __forceinline__ uint32_t v_off(int d, int g) {
+    return (uint32_t)(d * 128 + 8 * (g ^ ((d >> 1) & 15)));
+}
+
+struct PrefillParams {
+    const uint16_t *q;          // (T, H_q, 128) fp16, unrotated
+    uint16_t *out;              // (T, H_q, 128) fp16
+    const int32_t *cu_q;        // (B+1,)
+    const int32_t *seq_k;       // (B,) key length per sequence
+    int H_q, H_kv, GS;
+    float scale_log2;           // softmax scale * log2(e)
+    // paged source
+    const uint8_t *kv;
+    const int32_t *block_table;
+    int bt_stride, block_size, slot_bytes;
+    int64_t row_bytes;
+    const float *cb_k, *cb_v;
+    // dense source
+    const uint16_t *k_rot, *v_rot;
+    const int32_t *cu_k;        // (B+1,) first dense row of each sequence
+};
+
+// Registers holding one tile's share of the source data for this thread:
+// paged: K codes k[0..1] + nk, V codes v[0..3] (two bytes per key) + nv[];
+// dense: K fp16 k[0..7], V fp16 v[2i], v[2i+1] for key i.
+struct TileRegs {
+    uint32_t k[8];
+    uint32_t v[8];
+    float nk;
+    float nv[4];
+};
+
+template <bool PAGED>
+__device__ __forceinline__ void load_tile(const PrefillParams &p, TileRegs &r, int b, int h,
+                                          int kbase, int nk_valid, int tid) {
+    // K share: key tk = tid >> 3, dims [16c, 16c+16) with c = tid & 7.
+    // V share: keys 4g..4g+3 with g = tid >> 5, dims [4c, 4c+4) with c = tid & 31.
+    // Keys at or past nk_valid are not read (zeros; they are masked later).
+    const int tk = tid >> 3, ck = tid & 7;
+    const int gv = tid >> 5, cv = tid & 31;
+    if (PAGED) {
+        const int32_t *bt = p.block_table + (int64_t)b * p.bt_stride;
+        auto row = [&](int kpos) -> const uint8_t * {
+            const int64_t slot =
+                (int64_t)bt[kpos / p.block_size] * p.block_size + kpos % p.block_size;
+            return p.kv + slot * p.row_bytes + (int64_t)h * p.slot_bytes;
+        };
+        r.k[0] = r.k[1] = 0u;
+        r.nk = 0.0f;
+        if (tk < nk_valid) {
+            const uint8_t *rp = row(kbase + tk);
+            const uint2 w = *reinterpret_cast<const uint2 *>(rp + 8 * ck);
+            r.k[0] = w.x;
+            r.k[1] = w.y;
+            r.nk = *reinterpret_cast<const float *>(rp + 128);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int t = 4 * gv + i;
+            r.v[i] = 0u;
+            r.nv[i] = 0.0f;
+            if (t < nk_valid) {
+                const uint8_t *rp = row(kbase + t);
+                r.v[i] = *reinterpret_cast<const uint16_t *>(rp + 64 + 2 * cv);
+                r.nv[i] = *reinterpret_cast<const float *>(rp + 132);
+            }
+        }
+    } else {
+        const int64_t r0 = p.cu_k[b] + kbase;
+        const int64_t hs = (int64_t)p.H_kv * kD;
+        uint4 x0 = make_uint4(0, 0, 0, 0), x1 = x0;
+        if (tk < nk_valid) {
+            const uint4 *src =
+                reinterpret_cast<const uint4 *>(p.k_rot + (r0 + tk) * hs + h * kD + 16 * ck);
+            x0 = src[0];
+            x1 = src[1];
+        }
+        r.k[0] = x0.x; r.k[1] = x0.y; r.k[2] = x0.z; r.k[3] = x0.w;
+        r.k[4] = x1.x; r.k[5] = x1.y; r.k[6] = x1.z; r.k[7] = x1.w;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int t = 4 * gv + i;
+            uint2 v = make_uint2(0u, 0u);
+            if (t < nk_valid)
+                v = *reinterpret_cast<const uint2 *>(p.v_rot + (r0 + t) * hs + h * kD + 4 * cv);
+            r.v[2 * i] = v.x;
+            r.v[2 * i + 1] = v.y;
+        }
+    }
+}
+
+// One code byte's two values fp16(cb[code] * norm) from the per-code table
+// (16 rows x 64 lane columns of fp32).
+__device__ __forceinline__ uint32_t dq_pair(const uint8_t *lut, uint32_t byte, uint32_t col,
+                                           float norm) {
+    const float hi = *reinterpret_cast<const float *>(lut + ((byte >> 4) << 8) + col);
+    const float lo = *reinterpret_cast<const float *>(lut + ((byte & 15u) << 8) + col);
+    return cvt_pk(hi * norm, lo * norm);
+}
+
+template <bool PAGED>
+__device__ __forceinline__ void store_tile(const TileRegs &r, uint8_t *kt, uint8_t *vt,
+                                           const uint8_t *lutk, const uint8_t *lutv, int tid) {
+    const int tk = tid >> 3, ck = tid & 7;
+    const int gv = tid >> 5, cv = tid & 31;
+    const uint32_t col = (uint32_t)(tid & 63) * 4u;
+    uint32_t kw[8];      // key tk, dims [16ck, 16ck+16) as fp16 pairs (2j, 2j+1)
+    uint32_t pr[4][2];   // key 4gv+i: dims (4cv, 4cv+1), (4cv+2, 4cv+3) as fp16 pairs
+    if (PAGED) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const uint32_t byte = (r.k[j >> 2] >> (8 * (j & 3))) & 0xFFu;
+            kw[j] = dq_pair(lutk, byte, col, r.nk);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            pr[i][0] = dq_pair(lutv, r.v[i] & 0xFFu, col, r.nv[i]);
+            pr[i][1] = dq_pair(lutv, (r.v[i] >> 8) & 0xFFu, col, r.nv[i]);
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) kw[j] = r.k[j];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            pr[i][0] = r.v[2 * i];
+            pr[i][1] = r.v[2 * i + 1];
+        }
+    }
+    // V^T: dim 4cv+k gets keys 4gv..4gv+3 (a 4 x 4 fp16 transpose).
+    uint32_t vw[4][2];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const int w = k >> 1;
+        const uint32_t sel = (k & 1) ? 0x07060302u : 0x05040100u;
+        vw[k][0] = __builtin_amdgcn_perm(pr[1][w], pr[0][w], sel);
+        vw[k][1] = __builtin_amdgcn_perm(pr[3][w], pr[2][w], sel);
+    }
+#pragma unroll
+    for (int gi = 0; gi < 4; ++gi)
+        *reinterpret_cast<uint2 *>(kt + k_off(tk, 4 * ck + gi)) = make_uint2(kw[2 * gi], kw[2 * gi + 1]);
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+        *reinterpret_cast<uint2 *>(vt + v_off(4 * cv + k, gv)) = make_uint2(vw[k][0], vw[k][1]);
+}
+
+template <bool PAGED, int GS>
+__global__ void __launch_bounds__(kThreads, 1)
+prefill_kernel(PrefillParams p) {
+    __shared__ __align__(16) uint8_t smem[kPrefillLds];
+    constexpr int QB = 32 * (kWaves / GS);          // queries per workgroup
+
+    const int b = blockIdx.y;
+    const int h = blockIdx.z;
+    const int tid = threadIdx.x;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int lane = tid & 63;
+    const int u = lane >> 5;
+    const int c32 = lane & 31;
+
+    const int q_begin = p.cu_q[b];
+    const int seq_q = p.cu_q[b + 1] - q_begin;
+    const int seq_k = p.seq_k[b];
+    // Longest workgroups first: blockIdx.x counts query blocks from the end.
+    const int q0 = (gridDim.x - 1 - blockIdx.x) * QB;
+    if (q0 >= seq_q) return;
+    const int off = seq_k - seq_q;                   // bottom-right causal alignment
+    const int q_last = min(q0 + QB, seq_q) - 1;
+    const int kend = max(0, min(seq_k, q_last + off + 1));
+
+    const int hq = h * GS + wave % GS;
+    const int qw0 = q0 + 32 * (wave / GS);           // first query of this wave
+    const bool wave_live = qw0 < seq_q;
+    const int my_q = min(qw0 + c32, seq_q - 1);       // this lane's query (clamped)
+    const int my_kmax = min(seq_k, my_q + off + 1);   // keys [0, my_kmax) visible
+    const int wave_kend = wave_live ? max(0, min(seq_k, min(qw0 + 31, seq_q - 1) + off + 1)) : 0;
+    const int wave_kfull = max(0, min(seq_k, qw0 + off + 1));   // keys visible to every lane
+
+    // ---- tables for the paged source.
+    const uint8_t *lutk = smem + kLutOff;
+    const uint8_t *lutv = smem + kLutOff + kLutBytes / 2;
+    if (PAGED) {
+        float *lk = reinterpret_cast<float *>(smem + kLutOff);
+        for (int i = tid; i < 2 * 16 * 64; i += kThreads)
+            lk[i] = (i < 16 * 64) ? p.cb_k[i >> 6] : p.cb_v[(i - 16 * 64) >> 6];
+    }
+
+    // ---- prologue: q_rot^T = H q^T, rounded to fp16 (compression.py:290-291).
+    half8 qb[4][2];
+    {
+        const float hs = 0.08838834764831845f;       // 1/sqrt(128)
+        const uint16_t *qrow = p.q + ((int64_t)(q_begin + my_q) * p.H_q + hq) * kD;
+        half8 qin[8];
+#pragma unroll
+        for (int s = 0; s < 8; ++s)
+            qin[s] = *reinterpret_cast<const half8 *>(qrow + 16 * s + 8 * u);
+#pragma unroll
+        for (int T = 0; T < 4; ++T) {
+            floatx16 acc = {};
+#pragma unroll
+            for (int s = 0; s < 8; ++s) {
+                half8 a;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) a[e] = hsign(16 * s + 8 * u + e, 32 * T + c32);
+                acc = mfma32(a, qin[s], acc);
+            }
+            qb[T][0] = pack8(acc, 0, hs);
+            qb[T][1] = pack8(acc, 8, hs);
+        }
+    }
+
+    floatx16 o[4];
+#pragma unroll
+    for (int T = 0; T < 4; ++T) o[T] = floatx16{};
+    float m_run = -INFINITY, l_run = 0.0f;
+
+    const int ntiles = (kend + kBN - 1) / kBN;
+    TileRegs cur;
+    if (ntiles > 0) load_tile<PAGED>(p, cur, b, h, 0, min(kBN, kend), tid);
+    __syncthreads();   // tables visible
+
+    for (int j = 0; j < ntiles; ++j) {
+        uint8_t *kt = smem + (j & 1) * kTileBytes;
+        uint8_t *vt = kt + kBN * kD * 2;
+        store_tile<PAGED>(cur, kt, vt, lutk, lutv, tid);
+        if (j + 1 < ntiles)
+            load_tile<PAGED>(p, cur, b, h, (j + 1) * kBN, min(kBN, kend - (j + 1) * kBN), tid);
+        __syncthreads();
+
+        const int kbase = j * kBN;
+        if (!wave_live || kbase >= wave_kend) continue;
+        // ---- S^T for the two 32-key halves of the tile.
+        floatx16 st[2];
+        const bool live1 = kbase + 32 < wave_kend;
+#pragma unroll
+        for (int sub = 0; sub < 2; ++sub) {
+            st[sub] = floatx16{};
+            if (sub == 1 && !live1) continue;
+            const int t = 32 * sub + c32;
+#pragma unroll
+            for (int T = 0; T < 4; ++T)
+#pragma unroll
+                for (int s = 0; s < 2; ++s) {
+                    const int G = 8 * T + 4 * s + u;
+                    const uint2 x0 = *reinterpret_cast<const uint2 *>(kt + k_off(t, G));
+                    const uint2 x1 = *reinterpret_cast<const uint2 *>(kt + k_off(t, G + 2));
+                    const half8 a = __builtin_bit_cast(half8, make_uint4(x0.x, x0.y, x1.x, x1.y));
+                    st[sub] = mfma32(a, qb[T][s], st[sub]);
+                }
+        }
+        // ---- mask, online softmax (log2 domain).  Lane = one query; rows =
+        // keys kbase + 32*sub + (r%4) + 4u + 8(r/4).
+        const bool full = kbase + kBN <= wave_kfull;
+        float mt = -INFINITY;
+#pragma unroll
+        for (int sub = 0; sub < 2; ++sub)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                float x = st[sub][r] * p.scale_log2;
+                if (!full) {
+                    const int kpos = kbase + 32 * sub + (r & 3) + 4 * u + 8 * (r >> 2);
+                    if (kpos >= my_kmax || (sub == 1 && !live1)) x = -INFINITY;
+                }
+                st[sub][r] = x;
+                mt = fmaxf(mt, x);
+            }
+        {
+            auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mt), __float_as_uint(mt),
+                                                       false, false);
+            mt = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
+        }
+        const float m_new = fmaxf(m_run, mt);
+        const float m_sub = (m_new == -INFINITY) ? 0.0f : m_new;
+        const float alpha = __builtin_amdgcn_exp2f(m_run - m_sub);
+        m_run = m_new;
+        float ls = 0.0f;
+#pragma unroll
+        for (int sub = 0; sub < 2; ++sub)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const float e = __builtin_amdgcn_exp2f(st[sub][r] - m_sub);
+                st[sub][r] = e;
+                ls += e;
+            }
+        {
+            auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(ls), __float_as_uint(ls),
+                                                       false, false);
+            ls = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
+        }
+        l_run = l_run * alpha + ls;
+        if (alpha != 1.0f) {
+#pragma unroll
+            for (int T = 0; T < 4; ++T)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) o[T][r] *= alpha;
+        }
+        // ---- O^T += V^T P^T.
+#pragma unroll
+        for (int sub = 0; sub < 2; ++sub) {
+            if (sub == 1 && !live1) continue;
+#pragma unroll
+            for (int s = 0; s < 2; ++s) {
+                const half8 pb = pack8(st[sub], 8 * s, 1.0f);
+                const int g = 8 * sub + 4 * s + u;
+#pragma unroll
+                for (int T = 0; T < 4; ++T) {
+                    const int d = 32 * T + c32;
+                    const uint2 x0 = *reinterpret_cast<const uint2 *>(vt + v_off(d, g));
+                    const uint2 x1 = *reinterpret_cast<const uint2 *>(vt + v_off(d, g + 2));
+                    const half8 a = __builtin_bit_cast(half8, make_uint4(x0.x, x0.y, x1.x, x1.y));
+                    o[T] = mfma32(a, pb, o[T]);
+                }
+            }
+        }
+    }
+    if (!wave_live) return;
+
+    // ---- epilogue: O_rot = fp16(O / l) (attention.py:93), out = fp16(O_rot H).
+    const float inv_l = 1.0f / fmaxf(l_run, 1e-30f);
+    half8 ob[4][2];
+#pragma unroll
+    for (int T = 0; T < 4; ++T) {
+        ob[T][0] = pack8(o[T], 0, inv_l);
+        ob[T][1] = pack8(o[T], 8, inv_l);
+    }
+    const float hs = 0.08838834764831845f;
+    const bool store = qw0 + c32 < seq_q;
+    uint16_t *orow = p.out + ((int64_t)(q_begin + qw0 + c32) * p.H_q + hq) * kD;
+#pragma unroll
+    for (int T = 0; T < 4; ++T) {
+        floatx16 acc = {};
+#pragma unroll
+        for (int Td = 0; Td < 4; ++Td)
+#pragma unroll
+            for (int s = 0; s < 2; ++s) {
+                half8 a;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) a[e] = hsign(kdim(Td, s, u, e), 32 * T + c32);
+                acc = mfma32(a, ob[Td][s], acc);
+            }
+        if (store) {
+#pragma unroll
+            for (int gi = 0; gi < 4; ++gi) {
+                const uint2 v = make_uint2(cvt_pk(acc[4 * gi + 0] * hs, acc[4 * gi + 1] * hs),
+                                           cvt_pk(acc[4 * gi + 2] * hs, acc[4 * gi + 3] * hs));
+                *reinterpret_cast<uint2 *>(orow + 32 * T + 8 * gi + 4 * u) = v;
+            }
+        }
+    }
+}
+
+// Dense rotated K/V from the paged cache (fa2_cda.py:64-95): row b*max_seq + t
+// of (B*max_seq, H_kv, 128) fp16 = fp16(centroid * norm) for t < seq_lens[b],
+// zeros beyond.  One 256-thread block per (4 rows of one sequence); thread =
+// (row, head, 16-dim chunk); the per-code tables sit in LDS (64 lane columns).
+__global__ void __launch_bounds__(256)
+paged_to_dense_kernel(const uint8_t *kv, int64_t row_bytes, int slot_bytes, int H_kv,
+                      const int32_t *block_table, int bt_stride, const int32_t *seq_lens,
+                      const float *cb_k, const float *cb_v, int block_size, int max_seq,
+                      uint16_t *k_out, uint16_t *v_out) {
+    __shared__ float lut[2][16 * 64];
+    const int tid = threadIdx.x;
+    for (int i = tid; i < 2 * 16 * 64; i += 256)
+        lut[i >> 10][i & 1023] = (i < 1024) ? cb_k[(i & 1023) >> 6] : cb_v[(i & 1023) >> 6];
+    __syncthreads();
+    const int b = blockIdx.y;
+    const int n = min(seq_lens[b], bt_stride * block_size);
+    const uint32_t col = (uint32_t)(tid & 63) * 4u;
+    const uint8_t *lk = reinterpret_cast<const uint8_t *>(lut[0]);
+    const uint8_t *lv = reinterpret_cast<const uint8_t *>(lut[1]);
+    const int per_row = H_kv * 8;                       // threads per token row
+    for (int w = tid; w < 4 * per_row; w += 256) {
+        const int t = blockIdx.x * 4 + w / per_row;
+        if (t >= max_seq) break;
+        const int h = (w % per_row) >> 3, c = w & 7;    // dims [16c, 16c+16)
+        uint4 ko0 = make_uint4(0, 0, 0, 0), ko1 = ko0, vo0 = ko0, vo1 = ko0;
+        if (t < n) {
+            const int64_t slot =
+                (int64_t)block_table[(int64_t)b * bt_stride + t / block_size] * block_size + t % block_size;
+            const uint8_t *rp = kv + slot * row_bytes + (int64_t)h * slot_bytes;
+            const uint2 kc = *reinterpret_cast<const uint2 *>(rp + 8 * c);
+            const uint2 vc = *reinterpret_cast<const uint2 *>(rp + 64 + 8 * c);
+            const float nk = *reinterpret_cast<const float *>(rp + 128);
+            const float nv = *reinterpret_cast<const float *>(rp + 132);
+            uint32_t kw[8], vw[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const uint32_t kb = ((j < 4 ? kc.x : kc.y) >> (8 * (j & 3))) & 0xFFu;
+                const uint32_t vb = ((j < 4 ? vc.x : vc.y) >> (8 * (j & 3))) & 0xFFu;
+                kw[j] = dq_pair(lk, kb, col, nk);
+                vw[j] = dq_pair(lv, vb, col, nv);
+            }
+            ko0 = make_uint4(kw[0], kw[1], kw[2], kw[3]);
+            ko1 = make_uint4(kw[4], kw[5], kw[6], kw[7]);
+            vo0 = make_uint4(vw[0], vw[1], vw[2], vw[3]);
+            vo1 = make_uint4(vw[4], vw[5], vw[6], vw[7]);
+        }
+        const int64_t o = (((int64_t)b * max_seq + t) * H_kv + h) * kD + 16 * c;
+        reinterpret_cast<uint4 *>(k_out + o)[0] = ko0;
+        reinterpret_cast<uint4 *>(k_out + o)[1] = ko1;
+        reinterpret_cast<uint4 *>(v_out + o)[0] = vo0;
+        reinterpret_cast<uint4 *>(v_out + o)[1] = vo1;
+    }
+}
+
+// y = fp16(scale * x H) for rows of 128 fp16 (Sylvester order, natural index):
+// 16 lanes per row, 8 elements per lane; butterflies over index bits 0-2 in
+// registers and bits 3-6 across lanes, in fp32.
+__global__ void __launch_bounds__(256)
+hadamard128_kernel(const uint16_t *x, uint16_t *y, int64_t rows, float scale) {
+    const int64_t row = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4);
+    const int l16 = threadIdx.x & 15;
+    float v[8] = {};
+    if (row < rows) {
+        const uint4 w = *reinterpret_cast<const uint4 *>(x + row * kD + 8 * l16);
+        const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            v[2 * i] = h2f((uint16_t)(ws[i] & 0xFFFFu));
+            v[2 * i + 1] = h2f((uint16_t)(ws[i] >> 16));
+        }
+    }
+#pragma unroll
+    for (int m = 1; m < 8; m <<= 1)
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+            if (!(i & m)) {
+                const float a = v[i], c = v[i | m];
+                v[i] = a + c;
+                v[i | m] = a - c;
+            }
+#pragma unroll
+    for (int m = 1; m < 16; m <<= 1) {
+        const bool upper = (l16 & m) != 0;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const float o = __shfl_xor(v[i], m);
+            v[i] = upper ? (o - v[i]) : (v[i] + o);
+        }
+    }
+    if (row < rows) {
+        uint4 w;
+        w.x = cvt_pk(v[0] * scale, v[1] * scale);
+        w.y = cvt_pk(v[2] * scale, v[3] * scale);
+        w.z = cvt_pk(v[4] * scale, v[5] * scale);
+        w.w = cvt_pk(v[6] * scale, v[7] * scale);
+        *reinterpret_cast<uint4 *>(y + row * kD + 8 * l16) = w;
+    }
+}
+
+template <bool PAGED>
+int launch_prefill(const PrefillParams &p, int B, int max_q, hipStream_t st, const char *fn) {
+    const int qb = 32 * (kWaves / p.GS);
+    const dim3 grid((max_q + qb - 1) / qb, B, p.H_kv);
+    if (grid.x == 0) return CDA_OK;
+    if (p.GS == 4)
+        prefill_kernel<PAGED, 4><<<grid, kThreads, 0, st>>>(p);
+    else
+        prefill_kernel<PAGED, 8><<<grid, kThreads, 0, st>>>(p);
+    CDA_LAUNCH_CHECK(std::string(fn) + ": prefill_kernel");
+    return CDA_OK;
+}
+
+}  // namespace
+}  // namespace cda
+
+using namespace cda;
+
+extern "C" int cda_prefill_paged_hadamard(const void *q, const void *kv_cache, int64_t num_slots,
+                                          int slot_bytes, int H_kv, const int32_t *block_table,
+                                          int bt_stride, const int32_t *cu_seqlens_q,
+                                          const int32_t *seq_lens, int B, const float *cb_k,
+                                          const float *cb_v, int levels, void *out, int T,
+                                          int H_q, int block_size, int max_query_len,
+                                          float scale, void *stream) {
+    const char *fn = "cda_prefill_paged_hadamard";
+    (void)num_slots;
+    (void)T;
+    CDA_REQUIRE(q && kv_cache && block_table && cu_seqlens_q && seq_lens && cb_k && cb_v && out,
+                "cda_prefill_paged_hadamard: null pointer argument");
+    CDA_REQUIRE(B >= 0 && H_kv > 0 && H_q > 0 && max_query_len >= 0,
+                "cda_prefill_paged_hadamard: bad B / H_q / H_kv / max_query_len");
+    CDA_REQUIRE(H_q % H_kv == 0 && (H_q / H_kv == 4 || H_q / H_kv == 8),
+                "cda_prefill_paged_hadamard: H_q / H_kv must be 4 or 8");
+    CDA_REQUIRE(levels == 16 && slot_bytes >= 136,
+                "cda_prefill_paged_hadamard: the prefill reads K4V4 caches (16 levels, slot >= 136 B)");
+    CDA_REQUIRE(block_size > 0 && bt_stride > 0, "cda_prefill_paged_hadamard: bad block table");
+    CDA_REQUIRE(((uintptr_t)q & 15) == 0 && ((uintptr_t)out & 15) == 0 &&
+                    ((uintptr_t)kv_cache & 7) == 0 && slot_bytes % 8 == 0,
+                "cda_prefill_paged_hadamard: q/out must be 16-byte and the cache 8-byte aligned");
+    if (B == 0 || max_query_len == 0) return CDA_OK;
+    PrefillParams p{};
+    p.q = static_cast<const uint16_t *>(q);
+    p.out = static_cast<uint16_t *>(out);
+    p.cu_q = cu_seqlens_q;
+    p.seq_k = seq_lens;
+    p.H_q = H_q;
+    p.H_kv = H_kv;
+    p.GS = H_q / H_kv;
+    p.scale_log2 = scale * kLog2e;
+    p.kv = static_cast<const uint8_t *>(kv_cache);
+    p.block_table = block_table;
+    p.bt_stride = bt_stride;
+    p.block_size = block_size;
+    p.slot_bytes = slot_bytes;
+    p.row_bytes = (int64_t)H_kv * slot_bytes;
+    p.cb_k = cb_k;
+    p.cb_v = cb_v;
+    return launch_prefill<true>(p, B, max_query_len, static_cast<hipStream_t>(stream), fn);
+}
+
+extern "C" int cda_fa2_varlen_fwd_hadamard(const void *q, const void *k_rot, const void *v_rot,
+                                           void *out, const int32_t *cu_seqlens_q,
+                                           const int32_t *cu_seqlens_k, const int32_t *seqused_k,
+                                           int B, int T, int H_q, int H_kv, int max_query_len,
+                                           int max_seq_len, float scale, void *stream) {
+    const char *fn = "cda_fa2_varlen_fwd_hadamard";
+    (void)T;
+    (void)max_seq_len;
+    CDA_REQUIRE(q && k_rot && v_rot && out && cu_seqlens_q && cu_seqlens_k && seqused_k,
+                "cda_fa2_varlen_fwd_hadamard: null pointer argument");
+    CDA_REQUIRE(B >= 0 && H_kv > 0 && H_q > 0 && max_query_len >= 0,
+                "cda_fa2_varlen_fwd_hadamard: bad B / H_q / H_kv / max_query_len");
+    CDA_REQUIRE(H_q % H_kv == 0 && (H_q / H_kv == 4 || H_q / H_kv == 8),
+                "cda_fa2_varlen_fwd_hadamard: H_q / H_kv must be 4 or 8");
+    CDA_REQUIRE(((uintptr_t)q & 15) == 0 && ((uintptr_t)out & 15) == 0 &&
+                    ((uintptr_t)k_rot & 15) == 0 && ((uintptr_t)v_rot & 15) == 0,
+                "cda_fa2_varlen_fwd_hadamard: tensors must be 16-byte aligned");
+    if (B == 0 || max_query_len == 0) return CDA_OK;
+    PrefillParams p{};
+    p.q = static_cast<const uint16_t *>(q);
+    p.out = static_cast<uint16_t *>(out);
+    p.cu_q = cu_seqlens_q;
+    p.seq_k = seqused_k;
+    p.H_q = H_q;
+    p.H_kv = H_kv;
+    p.GS = H_q / H_kv;
+    p.scale_log2 = scale * kLog2e;
+    p.k_rot = static_cast<const uint16_t *>(k_rot);
+    p.v_rot = static_cast<const uint16_t *>(v_rot);
+    p.cu_k = cu_seqlens_k;
+    return launch_prefill<false>(p, B, max_query_len, static_cast<hipStream_t>(stream), fn);
+}
+
+extern "C" int cda_fa2_paged_cache_to_dense_rotated(const void *kv_cache, int64_t num_slots,
+                                                    int slot_bytes, int H_kv,
+                                                    const int32_t *block_table, int bt_stride,
+                                                    const int32_t *seq_lens, int B,
+                                                    const float *cb_k, const float *cb_v,
+                                                    int levels, int block_size, int max_seq_len,
+                                                    void *k_out, void *v_out, void *stream) {
+    (void)num_slots;
+    CDA_REQUIRE(kv_cache && block_table && seq_lens && cb_k && cb_v && k_out && v_out,
+                "cda_fa2_paged_cache_to_dense_rotated: null pointer argument");
+    CDA_REQUIRE(B >= 0 && H_kv > 0 && max_seq_len >= 0 && block_size > 0 && bt_stride > 0,
+                "cda_fa2_paged_cache_to_dense_rotated: bad shape arguments");
+    CDA_REQUIRE(levels == 16 && slot_bytes >= 136 && slot_bytes % 8 == 0,
+                "cda_fa2_paged_cache_to_dense_rotated: K4V4 caches only (16 levels, slot >= 136 B)");
+    CDA_REQUIRE(((uintptr_t)kv_cache & 7) == 0 && ((uintptr_t)k_out & 15) == 0 &&
+                    ((uintptr_t)v_out & 15) == 0,
+                "cda_fa2_paged_cache_to_dense_rotated: misaligned pointer");
+    if (B == 0 || max_seq_len == 0) return CDA_OK;
+    const dim3 grid((max_seq_len + 3) / 4, B);
+    paged_to_dense_kernel<<<grid, 256, 0, static_cast<hipStream_t>(stream)>>>(
+        static_cast<const uint8_t *>(kv_cache), (int64_t)H_kv * slot_bytes, slot_bytes, H_kv,
+        block_table, bt_stride, seq_lens, cb_k, cb_v, block_size, max_seq_len,
+        static_cast<uint16_t *>(k_out), static_cast<uint16_t *>(v_out));
+    CDA_LAUNCH_CHECK("paged_to_dense_kernel");
+    return CDA_OK;
+}
+
+extern "C" int cda_hadamard128_fp16(const void *x, void *y, int64_t rows, float scale,
+                                    void *stream) {
+    CDA_REQUIRE(x && y && rows >= 0, "cda_hadamard128_fp16: bad arguments");
+    CDA_REQUIRE(((uintptr_t)x & 15) == 0 && ((uintptr_t)y & 15) == 0,
+                "cda_hadamard128_fp16: x and y must be 16-byte aligned");
+    if (rows == 0) return CDA_OK;
+    hadamard128_kernel<<<(unsigned)((rows + 15) / 16), 256, 0, static_cast<hipStream_t>(stream)>>>(
+        static_cast<const uint16_t *>(x), static_cast<uint16_t *>(y), rows, scale);
+    CDA_LAUNCH_CHECK("hadamard128_kernel");
+    return CDA_OK;
+}

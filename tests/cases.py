@@ -61,3 +61,42 @@ def synth_cb():
         from pathlib import Path
         _CB = np.load(Path(__file__).parent / "golden" / "codebooks.npz")["lloyd_beta16"]
     return _CB
+
+
+@dataclass
+class PrefillCase:
+    q: np.ndarray            # (T, H_q, 128) fp16, T = sum(seq_q)
+    cu_q: np.ndarray         # (B+1,) int32
+    cache: np.ndarray
+    block_table: np.ndarray
+    seq_k: np.ndarray        # (B,) int32 key lengths
+    cb: np.ndarray
+    H_kv: int
+    block_size: int
+    expected: np.ndarray     # oracle output (T, H_q, 128) fp16
+
+
+def make_prefill_case(seed, seq_q, seq_k, *, H_kv=8, gs=4, block_size=16, scale=None, fill=0):
+    """Seeded K/V for each sequence's seq_k keys (encoded by the checker into a
+    paged cache), queries for its last seq_q positions, and the checker's
+    causal prefill output."""
+    seq_q = np.asarray(seq_q, dtype=np.int32)
+    seq_k = np.asarray(seq_k, dtype=np.int32)
+    B = len(seq_q)
+    H_q = H_kv * gs
+    cb = synth_cb()
+    nmax = max(1, int(seq_k.max()))
+    W = (nmax + block_size - 1) // block_size + 1
+    bt = synth.permuted_block_table(seed, B, W)
+    k = synth.kv_with_outliers(seed, (B, H_kv, nmax, D))
+    v = synth.normal_f16(seed + 1, (B, H_kv, nmax, D))
+    kp, kn, _ = O.encode(k, cb)
+    vp, vn, _ = O.encode(v, cb)
+    cache = O.build_paged_cache(kp, kn, vp, vn, bt, block_size, cb.size,
+                                num_blocks=B * W, fill=fill)
+    cu = np.concatenate([[0], np.cumsum(seq_q)]).astype(np.int32)
+    q = synth.normal_f16(seed + 2, (int(cu[-1]), H_q, D))
+    R = O.hadamard128()
+    exp = O.prefill_paged(q, cu, cache, bt, seq_k, cb, cb, R, H_kv=H_kv,
+                          block_size=block_size, scale=scale)
+    return PrefillCase(q, cu, cache, bt, seq_k, cb, H_kv, block_size, exp)
