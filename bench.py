@@ -81,6 +81,98 @@ def make_workload(B: int, N: int, dev, seed: int | None = None, identity_bt: boo
                 out=torch.empty_like(q), B=B, N=N)
 
 
+def make_prefill_workload(dev, seed: int = 0xCDA3, n_seq: int = 8, lo: int = 512,
+                          hi: int = 8192):
+    """n_seq sequences with lengths ~ U[lo, hi], all keys
+    new (causal prefill), K/V encoded into a paged K4V4 cache by the fused
+    encoder (K, V ~ N(0,1) fp16, K with 4 outlier channels x8), Q ~ N(0,1)."""
+    import torch
+    from sub0_amd import _native
+    from sub0_amd.cda.algorithm.compression import hadamard_matrix, lloyd_max_centroids_beta
+
+    cpu = torch.Generator().manual_seed(seed)
+    gpu = torch.Generator(device=dev).manual_seed(seed)
+    lens = torch.randint(lo, hi + 1, (n_seq,), generator=cpu).tolist()
+    nbs = [(L + BS - 1) // BS for L in lens]
+    W = max(nbs)
+    perm = torch.randperm(sum(nbs), generator=cpu).to(torch.int32)
+    bt = torch.zeros(n_seq, W, dtype=torch.int32)
+    o = 0
+    for i, nb in enumerate(nbs):
+        bt[i, :nb] = perm[o:o + nb]
+        o += nb
+    bt = bt.to(dev)
+    outl = torch.randperm(D, generator=cpu)[:4].to(dev)
+    cache = torch.zeros(sum(nbs) * BS, H_KV, 144, dtype=torch.uint8, device=dev)
+    cb = lloyd_max_centroids_beta(16, D).to(dev)
+    for i, L in enumerate(lens):
+        pos = torch.arange(L, device=dev, dtype=torch.int64)
+        slots = (bt[i, pos // BS].to(torch.int64) * BS + pos % BS).to(torch.int32)
+        k = torch.randn(L, H_KV, D, generator=gpu, device=dev, dtype=torch.float16)
+        k[..., outl] *= 8
+        v = torch.randn(L, H_KV, D, generator=gpu, device=dev, dtype=torch.float16)
+        _native.paged_encode(k, v, slots, cache, cb, cb)
+    T = sum(lens)
+    q = torch.randn(T, H_Q, D, generator=gpu, device=dev, dtype=torch.float16)
+    cu = torch.tensor([0] + list(torch.tensor(lens).cumsum(0).tolist()), dtype=torch.int32,
+                      device=dev)
+    seq = torch.tensor(lens, dtype=torch.int32, device=dev)
+    torch.cuda.synchronize()
+    # causal pairs (k <= q) per head: L(L+1)/2; QK and PV are 2*D flops each per pair
+    flops = sum(4 * H_Q * D * (L * (L + 1) // 2) for L in lens)
+    return dict(q=q, cache=cache, bt=bt, cu=cu, seq=seq, cb=cb, R=hadamard_matrix(D).to(dev),
+                out=torch.empty_like(q), lens=lens, T=T, flops=flops)
+
+
+def prefill_call(w, dense: bool = False):
+    from sub0_amd.cda.kernels_cuda.fa2_cda import fa2_cda_prefill_varlen_v1
+
+    def call():
+        fa2_cda_prefill_varlen_v1(w["q"], w["cache"], w["bt"], w["cu"], w["seq"], w["out"],
+                                  cb_K=w["cb"], cb_V=w["cb"], rotation_fp32=w["R"],
+                                  group_size=H_Q // H_KV, block_size=BS,
+                                  max_query_len=max(w["lens"]), max_seq_len=max(w["lens"]),
+                                  fuse_fa2_epilogue=True, return_dense_kv=dense)
+    return call
+
+
+def prefill_main(args) -> int:
+    """--prefill: BASELINE config 3 (not the headline metric); one JSON line."""
+    import torch
+    dev = torch.device("cuda:0")
+    w = make_prefill_workload(dev)
+    res = {}
+    for name, dense in (("compressed_tiles", False), ("dense_bridge", True)):
+        g = capture(prefill_call(w, dense), args.warmup)
+        for _ in range(args.warmup):
+            g.replay()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            g.replay()
+        torch.cuda.synchronize()
+        res[name] = (time.perf_counter() - t0) / args.steps * 1e3
+        del g
+    ms = res["compressed_tiles"]
+    tflops = w["flops"] / (ms * 1e-3) / 1e12
+    peak = 2500.0
+    line = {
+        "metric": "prefill TFLOP/s, causal varlen from the K4V4 cache (BASELINE config 3)",
+        "value": round(tflops, 1), "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": True,
+        "dtype": "fp16 MFMA operands, fp32 accumulate", "data": "synthetic",
+        "config": {"workload": "8 sequences, lengths ~ U[512, 8192], causal, 32 Q / 8 KV heads, "
+                               "d=128, K4V4 paged cache (block 16, permuted)",
+                   "lengths": w["lens"], "tokens": w["T"], "flops": w["flops"]},
+        "roofline": {"bound": "mfma", "achieved": round(tflops, 1), "peak": peak,
+                     "unit": "TFLOP/s", "frac": round(tflops / peak, 4),
+                     "kernel": "prefill_kernel<paged>"},
+        "dense_bridge_ms": round(res["dense_bridge"], 4),
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
 def decode_call(w, tile_n: int = 0):
     from sub0_amd.cda.kernels_cuda.wrappers import decode_hmma_v1
 
@@ -227,6 +319,8 @@ def main(argv=None):
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--tile-n", type=int, default=0,
                     help="tokens per split-K partition (0 = the library's plan)")
+    ap.add_argument("--prefill", action="store_true",
+                    help="time BASELINE config 3 (varlen causal prefill) instead of decode")
     ap.add_argument("--general-kernel", action="store_true",
                     help="forbid the page-streaming split kernel (A/B diagnostic)")
     ap.add_argument("--identity-block-table", action="store_true",
@@ -254,6 +348,8 @@ def main(argv=None):
         return 0
     from sub0_amd import _native
     _native.lib()
+    if args.prefill:
+        return prefill_main(args)
     if args.general_kernel:
         _native.set_stream_kernel(False)
     B, N = args.B, args.N

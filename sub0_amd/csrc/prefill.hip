@@ -28,6 +28,7 @@
 #include "cda_common.h"
 
 #include <cmath>
+#include <type_traits>
 
 namespace cda {
 namespace {
@@ -41,26 +42,25 @@ constexpr int kWaves = 8;
 constexpr int kThreads = 64 * kWaves;
 constexpr float kLog2e = 1.4426950408889634f;
 
-// LDS: two tile buffers (K [64 keys][128 dims] and V^T [128 dims][64 keys],
-// fp16, 16 KiB each), then the per-code dequant tables (paged source).
-constexpr int kTileBytes = 2 * kBN * kD * 2;
-constexpr int kLutOff = 2 * kTileBytes;               // 64 KiB
+// LDS: two tile buffers, then the per-code dequant tables (paged source).
+//   K tile   [64 keys][128 dims] fp16, natural dim order, rows padded to 272 B.
+//   V^T tile [128 dims][64 keys] fp16, rows padded to 144 B; within each
+//            16-key group the keys are stored in the MFMA k order (key
+//            8*jh + 4*u + jl at position 8*u + 4*jh + jl), so each MFMA
+//            operand is one 16-byte read.
+// The padding puts the 16 lanes of every 16-byte read (consecutive rows) in
+// distinct banks, and every address is a per-lane base plus a compile-time
+// offset.
+constexpr int kKRow = kD * 2 + 16;                     // 272
+constexpr int kVRow = kBN * 2 + 16;                    // 144
+constexpr int kKTile = kBN * kKRow;                    // 17408
+constexpr int kTileBytes = kKTile + kD * kVRow;         // + 18432
+constexpr int kLutOff = 2 * kTileBytes;
 constexpr int kLutBytes = 2 * 16 * 64 * 4;             // K and V, 16 codes x 64 columns
 constexpr int kPrefillLds = kLutOff + kLutBytes;
 
 __device__ __forceinline__ floatx16 mfma32(half8 a, half8 b, floatx16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
-}
-
-// Unnormalised Sylvester Hadamard entry (+-1): H[i][j] = (-1)^popcount(i & j).
-__device__ __forceinline__ _Float16 hsign(int i, int j) {
-    return (__builtin_popcount(i & j) & 1) ? (_Float16)-1.0f : (_Float16)1.0f;
-}
-
-// Dimension carried by k slot j of k-step (T, s) in lane half u: the row of the
-// 32x32 accumulator register 8s + j of tile T.
-__device__ __forceinline__ int kdim(int T, int s, int u, int j) {
-    return 32 * T + 16 * s + 8 * (j >> 2) + 4 * u + (j & 3);
 }
 
 __device__ __forceinline__ uint32_t cvt_pk(float a, float b) {
@@ -69,21 +69,56 @@ __device__ __forceinline__ uint32_t cvt_pk(float a, float b) {
     return __builtin_bit_cast(uint32_t, __builtin_convertvector(f2{a, b}, h2));
 }
 
-__device__ __forceinline__ half8 pack8(const floatx16 &c, int base, float scale) {
-    const uint4 v = make_uint4(cvt_pk(c[base + 0] * scale, c[base + 1] * scale),
-                               cvt_pk(c[base + 2] * scale, c[base + 3] * scale),
-                               cvt_pk(c[base + 4] * scale, c[base + 5] * scale),
-                               cvt_pk(c[base + 6] * scale, c[base + 7] * scale));
+__device__ __forceinline__ half8 pack8(const floatx16 &c, int base) {
+    const uint4 v = make_uint4(cvt_pk(c[base + 0], c[base + 1]), cvt_pk(c[base + 2], c[base + 3]),
+                               cvt_pk(c[base + 4], c[base + 5]), cvt_pk(c[base + 6], c[base + 7]));
     return __builtin_bit_cast(half8, v);
 }
 
-// K tile: key t's 4-dim group G (8 bytes) at t*256 + 8*(G ^ (t & 31)).
-__device__ __forceinline__ uint32_t k_off(int t, int G) {
-    return (uint32_t)(t * 256 + 8 * (G ^ (t & 31)));
+// Thread -> V share: dims [4cv, 4cv+4) of keys [4gv, 4gv+4).  Each 32-lane
+// half of a wave covers 4 cv x 8 gv, so its 8-byte V^T writes land in 32
+// distinct bank pairs.
+__device__ __forceinline__ int v_cv(int tid) { return (((tid >> 5) & 7) << 2) | ((tid >> 3) & 3); }
+__device__ __forceinline__ int v_gv(int tid) { return ((tid >> 8) << 3) | (tid & 7); }
+// Byte offset of keys 4gv..4gv+3 (8 bytes) in a V^T row.
+__device__ __forceinline__ uint32_t v_key_off(int gv) {
+    return (uint32_t)(32 * (gv >> 2) + 16 * (gv & 1) + 8 * ((gv >> 1) & 1));
 }
-// V^T tile: dim d's 4-key group g at d*128 + 8*(g ^ ((d >> 1) & 15)).
-__device__ __forceinline__ uint32_t v_off(int d, int g) {
-    return (uint32_t)(d * 128 + 8 * (g ^ ((d >> 1) & 15)));
+
+// A operand of a product with the unnormalised Hadamard matrix,
+// A[r][k] = (-1)^popcount(k & r) for r = 32*T + c32 and k = 16*S + 8*u + e:
+// the e part depends on the lane only (hbase), the rest flips all eight signs.
+__device__ __forceinline__ half8 hadamard_operand(uint4 hbase, int S, int u, int T, int c32) {
+    const uint32_t f = (__builtin_popcount((16 * S + 8 * u) & (32 * T + c32)) & 1) ? 0x80008000u : 0u;
+    return __builtin_bit_cast(half8, make_uint4(hbase.x ^ f, hbase.y ^ f, hbase.z ^ f, hbase.w ^ f));
+}
+
+__device__ __forceinline__ uint4 hadamard_base(int c32) {
+    uint32_t w[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t lo = (__builtin_popcount((2 * i) & c32 & 7) & 1) ? 0xBC00u : 0x3C00u;
+        const uint32_t hi = (__builtin_popcount((2 * i + 1) & c32 & 7) & 1) ? 0xBC00u : 0x3C00u;
+        w[i] = lo | (hi << 16);
+    }
+    return make_uint4(w[0], w[1], w[2], w[3]);
+}
+
+// B operand (natural k: values 16*S + 8*u + 0..7) of tile T's k-step S = 2T + s
+// from a 32x32 accumulator whose rows carry those values in MFMA row order
+// (row 8*g + 4*u + i in register 4*g + i of lane half u): lane half u keeps
+// its own group 2s+u and takes the partner half's, scaled by `scale`.
+__device__ __forceinline__ half8 acc_to_operand(const floatx16 &c, int s, int u, float scale) {
+    const int g0 = 2 * s, g1 = 2 * s + 1;
+    const uint32_t m0 = cvt_pk(c[4 * g0 + 0] * scale, c[4 * g0 + 1] * scale);
+    const uint32_t m1 = cvt_pk(c[4 * g0 + 2] * scale, c[4 * g0 + 3] * scale);
+    const uint32_t n0 = cvt_pk(c[4 * g1 + 0] * scale, c[4 * g1 + 1] * scale);
+    const uint32_t n1 = cvt_pk(c[4 * g1 + 2] * scale, c[4 * g1 + 3] * scale);
+    const uint32_t own0 = u ? n0 : m0, own1 = u ? n1 : m1;     // group 2s+u
+    const uint32_t snd0 = u ? m0 : n0, snd1 = u ? m1 : n1;     // what the partner needs
+    const uint32_t rcv0 = __shfl_xor(snd0, 32), rcv1 = __shfl_xor(snd1, 32);
+    const uint4 v = u ? make_uint4(rcv0, rcv1, own0, own1) : make_uint4(own0, own1, rcv0, rcv1);
+    return __builtin_bit_cast(half8, v);
 }
 
 struct PrefillParams {
@@ -97,6 +132,7 @@ struct PrefillParams {
     const uint8_t *kv;
     const int32_t *block_table;
     int bt_stride, block_size, slot_bytes;
+    int bs_shift;               // log2(block_size) when it is a power of two, else -1
     int64_t row_bytes;
     const float *cb_k, *cb_v;
     // dense source
@@ -121,12 +157,19 @@ __device__ __forceinline__ void load_tile(const PrefillParams &p, TileRegs &r, i
     // V share: keys 4g..4g+3 with g = tid >> 5, dims [4c, 4c+4) with c = tid & 31.
     // Keys at or past nk_valid are not read (zeros; they are masked later).
     const int tk = tid >> 3, ck = tid & 7;
-    const int gv = tid >> 5, cv = tid & 31;
+    const int gv = v_gv(tid), cv = v_cv(tid);
     if (PAGED) {
         const int32_t *bt = p.block_table + (int64_t)b * p.bt_stride;
         auto row = [&](int kpos) -> const uint8_t * {
-            const int64_t slot =
-                (int64_t)bt[kpos / p.block_size] * p.block_size + kpos % p.block_size;
+            int blk, in;
+            if (p.bs_shift >= 0) {
+                blk = kpos >> p.bs_shift;
+                in = kpos & (p.block_size - 1);
+            } else {
+                blk = kpos / p.block_size;
+                in = kpos - blk * p.block_size;
+            }
+            const int64_t slot = (int64_t)bt[blk] * p.block_size + in;
             return p.kv + slot * p.row_bytes + (int64_t)h * p.slot_bytes;
         };
         r.k[0] = r.k[1] = 0u;
@@ -186,7 +229,7 @@ template <bool PAGED>
 __device__ __forceinline__ void store_tile(const TileRegs &r, uint8_t *kt, uint8_t *vt,
                                            const uint8_t *lutk, const uint8_t *lutv, int tid) {
     const int tk = tid >> 3, ck = tid & 7;
-    const int gv = tid >> 5, cv = tid & 31;
+    const int gv = v_gv(tid), cv = v_cv(tid);
     const uint32_t col = (uint32_t)(tid & 63) * 4u;
     uint32_t kw[8];      // key tk, dims [16ck, 16ck+16) as fp16 pairs (2j, 2j+1)
     uint32_t pr[4][2];   // key 4gv+i: dims (4cv, 4cv+1), (4cv+2, 4cv+3) as fp16 pairs
@@ -219,12 +262,13 @@ __device__ __forceinline__ void store_tile(const TileRegs &r, uint8_t *kt, uint8
         vw[k][0] = __builtin_amdgcn_perm(pr[1][w], pr[0][w], sel);
         vw[k][1] = __builtin_amdgcn_perm(pr[3][w], pr[2][w], sel);
     }
-#pragma unroll
-    for (int gi = 0; gi < 4; ++gi)
-        *reinterpret_cast<uint2 *>(kt + k_off(tk, 4 * ck + gi)) = make_uint2(kw[2 * gi], kw[2 * gi + 1]);
+    uint4 *kd = reinterpret_cast<uint4 *>(kt + tk * kKRow + 32 * ck);
+    kd[0] = make_uint4(kw[0], kw[1], kw[2], kw[3]);
+    kd[1] = make_uint4(kw[4], kw[5], kw[6], kw[7]);
+    const uint32_t vo = v_key_off(gv);
 #pragma unroll
     for (int k = 0; k < 4; ++k)
-        *reinterpret_cast<uint2 *>(vt + v_off(4 * cv + k, gv)) = make_uint2(vw[k][0], vw[k][1]);
+        *reinterpret_cast<uint2 *>(vt + (4 * cv + k) * kVRow + vo) = make_uint2(vw[k][0], vw[k][1]);
 }
 
 template <bool PAGED, int GS>
@@ -268,27 +312,25 @@ prefill_kernel(PrefillParams p) {
             lk[i] = (i < 16 * 64) ? p.cb_k[i >> 6] : p.cb_v[(i - 16 * 64) >> 6];
     }
 
-    // ---- prologue: q_rot^T = H q^T, rounded to fp16 (compression.py:290-291).
-    half8 qb[4][2];
+    // ---- prologue: q_rot = fp16(q H / sqrt(128)) (compression.py:290-291) as
+    // the B operand of S^T = K q_rot^T, natural k (dims 16S + 8u + 0..7).
+    const float hs = 0.08838834764831845f;          // 1/sqrt(128)
+    const uint4 hbase = hadamard_base(c32);
+    half8 qb[8];
     {
-        const float hs = 0.08838834764831845f;       // 1/sqrt(128)
         const uint16_t *qrow = p.q + ((int64_t)(q_begin + my_q) * p.H_q + hq) * kD;
         half8 qin[8];
 #pragma unroll
-        for (int s = 0; s < 8; ++s)
-            qin[s] = *reinterpret_cast<const half8 *>(qrow + 16 * s + 8 * u);
+        for (int S = 0; S < 8; ++S)
+            qin[S] = *reinterpret_cast<const half8 *>(qrow + 16 * S + 8 * u);
 #pragma unroll
         for (int T = 0; T < 4; ++T) {
             floatx16 acc = {};
 #pragma unroll
-            for (int s = 0; s < 8; ++s) {
-                half8 a;
-#pragma unroll
-                for (int e = 0; e < 8; ++e) a[e] = hsign(16 * s + 8 * u + e, 32 * T + c32);
-                acc = mfma32(a, qin[s], acc);
-            }
-            qb[T][0] = pack8(acc, 0, hs);
-            qb[T][1] = pack8(acc, 8, hs);
+            for (int S = 0; S < 8; ++S)
+                acc = mfma32(hadamard_operand(hbase, S, u, T, c32), qin[S], acc);
+            qb[2 * T] = acc_to_operand(acc, 0, u, hs);
+            qb[2 * T + 1] = acc_to_operand(acc, 1, u, hs);
         }
     }
 
@@ -297,130 +339,139 @@ prefill_kernel(PrefillParams p) {
     for (int T = 0; T < 4; ++T) o[T] = floatx16{};
     float m_run = -INFINITY, l_run = 0.0f;
 
+    // Per-lane LDS bases: K rows 32*sub + c32 (16 bytes at dims 16S + 8u), V^T
+    // rows 32*T + c32 (16 bytes at key group 2*sub + s, half u).
+    const uint32_t k_lane = (uint32_t)(c32 * kKRow + 16 * u);
+    const uint32_t v_lane = (uint32_t)(kKTile + c32 * kVRow + 16 * u);
+
+    // One 64-key tile as two 32-key halves, software-pipelined so that the
+    // softmax (VALU) of one half runs while the MFMAs of the other are in
+    // flight: QK(0), QK(1) | softmax(0) | PV(0) | softmax(1) | PV(1).
+    // S^T = K q_rot^T; online softmax in the log2 domain with a lazy rescale
+    // (the running max moves only when a half's max exceeds it by more than
+    // 8, so P <= 2^8 and the O rescale is rare after the first tiles);
+    // O^T += V^T P^T.  MASK: the tile crosses the causal diagonal or the end
+    // of the keys.
+    auto qk = [&](const uint8_t *buf, int sub) {
+        half8 a[8];
+#pragma unroll
+        for (int S = 0; S < 8; ++S)
+            a[S] = *reinterpret_cast<const half8 *>(buf + k_lane + sub * 32 * kKRow + 32 * S);
+        floatx16 acc = {};
+#pragma unroll
+        for (int S = 0; S < 8; ++S) acc = mfma32(a[S], qb[S], acc);
+        return acc;
+    };
+    // Softmax of one half in place (st <- P); rows = keys kbase + 32*sub +
+    // (r%4) + 4u + 8(r/4), lane = one query.
+    auto softmax = [&](floatx16 &st, int kbase, int sub, auto masked) {
+        constexpr bool MASK = decltype(masked)::value;
+        float mt = -INFINITY;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            float x = st[r] * p.scale_log2;
+            if (MASK) {
+                const int kpos = kbase + 32 * sub + (r & 3) + 4 * u + 8 * (r >> 2);
+                if (kpos >= my_kmax) x = -INFINITY;
+            }
+            st[r] = x;
+            mt = fmaxf(mt, x);
+        }
+        {
+            auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mt), __float_as_uint(mt),
+                                                       false, false);
+            mt = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
+        }
+        // Wave-uniform branch (lanes that do not move scale by 1): a per-lane
+        // branch would be if-converted into a select over all of O.
+        const bool move = mt > m_run + 8.0f;
+        if (__builtin_amdgcn_ballot_w64(move)) {
+            const float alpha = move ? __builtin_amdgcn_exp2f(m_run - mt) : 1.0f;  // -inf -> 0
+            m_run = move ? mt : m_run;
+            l_run *= alpha;
+#pragma unroll
+            for (int T = 0; T < 4; ++T)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) o[T][r] *= alpha;
+        }
+        const float m_sub = (m_run == -INFINITY) ? 0.0f : m_run;
+        float ls = 0.0f;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const float e = __builtin_amdgcn_exp2f(st[r] - m_sub);
+            st[r] = e;
+            ls += e;
+        }
+        auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(ls), __float_as_uint(ls),
+                                                   false, false);
+        l_run += __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
+    };
+    auto pv = [&](const uint8_t *buf, const floatx16 &pt, int sub) {
+        half8 a[2][4];
+#pragma unroll
+        for (int s2 = 0; s2 < 2; ++s2)
+#pragma unroll
+            for (int T = 0; T < 4; ++T)
+                a[s2][T] = *reinterpret_cast<const half8 *>(
+                    buf + v_lane + T * 32 * kVRow + 32 * (2 * sub + s2));
+#pragma unroll
+        for (int s2 = 0; s2 < 2; ++s2) {
+            const half8 pb = pack8(pt, 8 * s2);
+#pragma unroll
+            for (int T = 0; T < 4; ++T) o[T] = mfma32(a[s2][T], pb, o[T]);
+        }
+    };
+    auto tile = [&](const uint8_t *buf, int kbase, auto masked) {
+        constexpr bool MASK = decltype(masked)::value;
+        const bool live1 = !MASK || kbase + 32 < wave_kend;
+        floatx16 s0 = qk(buf, 0);
+        softmax(s0, kbase, 0, masked);
+        pv(buf, s0, 0);
+        if (live1) {
+            floatx16 s1 = qk(buf, 1);
+            softmax(s1, kbase, 1, masked);
+            pv(buf, s1, 1);
+        }
+    };
+
     const int ntiles = (kend + kBN - 1) / kBN;
     TileRegs cur;
     if (ntiles > 0) load_tile<PAGED>(p, cur, b, h, 0, min(kBN, kend), tid);
     __syncthreads();   // tables visible
 
     for (int j = 0; j < ntiles; ++j) {
-        uint8_t *kt = smem + (j & 1) * kTileBytes;
-        uint8_t *vt = kt + kBN * kD * 2;
-        store_tile<PAGED>(cur, kt, vt, lutk, lutv, tid);
+        uint8_t *buf = smem + (j & 1) * kTileBytes;
+        store_tile<PAGED>(cur, buf, buf + kKTile, lutk, lutv, tid);
         if (j + 1 < ntiles)
             load_tile<PAGED>(p, cur, b, h, (j + 1) * kBN, min(kBN, kend - (j + 1) * kBN), tid);
         __syncthreads();
-
         const int kbase = j * kBN;
         if (!wave_live || kbase >= wave_kend) continue;
-        // ---- S^T for the two 32-key halves of the tile.
-        floatx16 st[2];
-        const bool live1 = kbase + 32 < wave_kend;
-#pragma unroll
-        for (int sub = 0; sub < 2; ++sub) {
-            st[sub] = floatx16{};
-            if (sub == 1 && !live1) continue;
-            const int t = 32 * sub + c32;
-#pragma unroll
-            for (int T = 0; T < 4; ++T)
-#pragma unroll
-                for (int s = 0; s < 2; ++s) {
-                    const int G = 8 * T + 4 * s + u;
-                    const uint2 x0 = *reinterpret_cast<const uint2 *>(kt + k_off(t, G));
-                    const uint2 x1 = *reinterpret_cast<const uint2 *>(kt + k_off(t, G + 2));
-                    const half8 a = __builtin_bit_cast(half8, make_uint4(x0.x, x0.y, x1.x, x1.y));
-                    st[sub] = mfma32(a, qb[T][s], st[sub]);
-                }
-        }
-        // ---- mask, online softmax (log2 domain).  Lane = one query; rows =
-        // keys kbase + 32*sub + (r%4) + 4u + 8(r/4).
-        const bool full = kbase + kBN <= wave_kfull;
-        float mt = -INFINITY;
-#pragma unroll
-        for (int sub = 0; sub < 2; ++sub)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                float x = st[sub][r] * p.scale_log2;
-                if (!full) {
-                    const int kpos = kbase + 32 * sub + (r & 3) + 4 * u + 8 * (r >> 2);
-                    if (kpos >= my_kmax || (sub == 1 && !live1)) x = -INFINITY;
-                }
-                st[sub][r] = x;
-                mt = fmaxf(mt, x);
-            }
-        {
-            auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mt), __float_as_uint(mt),
-                                                       false, false);
-            mt = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
-        }
-        const float m_new = fmaxf(m_run, mt);
-        const float m_sub = (m_new == -INFINITY) ? 0.0f : m_new;
-        const float alpha = __builtin_amdgcn_exp2f(m_run - m_sub);
-        m_run = m_new;
-        float ls = 0.0f;
-#pragma unroll
-        for (int sub = 0; sub < 2; ++sub)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const float e = __builtin_amdgcn_exp2f(st[sub][r] - m_sub);
-                st[sub][r] = e;
-                ls += e;
-            }
-        {
-            auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(ls), __float_as_uint(ls),
-                                                       false, false);
-            ls = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
-        }
-        l_run = l_run * alpha + ls;
-        if (alpha != 1.0f) {
-#pragma unroll
-            for (int T = 0; T < 4; ++T)
-#pragma unroll
-                for (int r = 0; r < 16; ++r) o[T][r] *= alpha;
-        }
-        // ---- O^T += V^T P^T.
-#pragma unroll
-        for (int sub = 0; sub < 2; ++sub) {
-            if (sub == 1 && !live1) continue;
-#pragma unroll
-            for (int s = 0; s < 2; ++s) {
-                const half8 pb = pack8(st[sub], 8 * s, 1.0f);
-                const int g = 8 * sub + 4 * s + u;
-#pragma unroll
-                for (int T = 0; T < 4; ++T) {
-                    const int d = 32 * T + c32;
-                    const uint2 x0 = *reinterpret_cast<const uint2 *>(vt + v_off(d, g));
-                    const uint2 x1 = *reinterpret_cast<const uint2 *>(vt + v_off(d, g + 2));
-                    const half8 a = __builtin_bit_cast(half8, make_uint4(x0.x, x0.y, x1.x, x1.y));
-                    o[T] = mfma32(a, pb, o[T]);
-                }
-            }
-        }
+        if (kbase + kBN <= wave_kfull) tile(buf, kbase, std::false_type{});
+        else tile(buf, kbase, std::true_type{});
     }
     if (!wave_live) return;
 
-    // ---- epilogue: O_rot = fp16(O / l) (attention.py:93), out = fp16(O_rot H).
+    // ---- epilogue: O_rot = fp16(O / l) (attention.py:93), out = fp16(O_rot H / sqrt(128)).
     const float inv_l = 1.0f / fmaxf(l_run, 1e-30f);
-    half8 ob[4][2];
+    half8 ob[8];
 #pragma unroll
     for (int T = 0; T < 4; ++T) {
-        ob[T][0] = pack8(o[T], 0, inv_l);
-        ob[T][1] = pack8(o[T], 8, inv_l);
+        ob[2 * T] = acc_to_operand(o[T], 0, u, inv_l);
+        ob[2 * T + 1] = acc_to_operand(o[T], 1, u, inv_l);
     }
-    const float hs = 0.08838834764831845f;
     const bool store = qw0 + c32 < seq_q;
     uint16_t *orow = p.out + ((int64_t)(q_begin + qw0 + c32) * p.H_q + hq) * kD;
+    // A fresh (opaque) copy of the Hadamard base, so the compiler rebuilds the
+    // operands here instead of keeping the prologue's 32 of them (128 VGPRs)
+    // alive through the key loop.
+    uint4 hb2 = hbase;
+    asm volatile("" : "+v"(hb2.x), "+v"(hb2.y), "+v"(hb2.z), "+v"(hb2.w));
 #pragma unroll
     for (int T = 0; T < 4; ++T) {
         floatx16 acc = {};
 #pragma unroll
-        for (int Td = 0; Td < 4; ++Td)
-#pragma unroll
-            for (int s = 0; s < 2; ++s) {
-                half8 a;
-#pragma unroll
-                for (int e = 0; e < 8; ++e) a[e] = hsign(kdim(Td, s, u, e), 32 * T + c32);
-                acc = mfma32(a, ob[Td][s], acc);
-            }
+        for (int S = 0; S < 8; ++S) acc = mfma32(hadamard_operand(hb2, S, u, T, c32), ob[S], acc);
         if (store) {
 #pragma unroll
             for (int gi = 0; gi < 4; ++gi) {
@@ -585,6 +636,7 @@ extern "C" int cda_prefill_paged_hadamard(const void *q, const void *kv_cache, i
     p.block_table = block_table;
     p.bt_stride = bt_stride;
     p.block_size = block_size;
+    p.bs_shift = (block_size & (block_size - 1)) == 0 ? __builtin_ctz(block_size) : -1;
     p.slot_bytes = slot_bytes;
     p.row_bytes = (int64_t)H_kv * slot_bytes;
     p.cb_k = cb_k;
