@@ -5,26 +5,28 @@
 // 426-482 (attention_compressed), split-K partials and merge of :190-272.
 //
 // Three launches on the caller's stream:
-//   1. rotate_q:  q_rot = fp16(q @ R) per (b, q-head); block (0,0) also writes
-//                 R^T into the workspace for the epilogue.
+//   1. rotate_q:  q_rot = fp16(q @ R) per (b, q-head).
 //   2. split:     one workgroup per (b, context split, group of 8 KV heads);
-//                 wave w owns KV head 8*blockIdx.y + w and its GQA group.  Each
-//                 wave streams its split 32 tokens at a time straight from HBM
-//                 (K codes as one 16-byte load per lane per 16 tokens, V codes
-//                 and norms as dword loads) and dequantises through LDS tables
-//                 indexed by code byte, one table column per lane so reads do
-//                 not conflict.  K is rebuilt as fp16(centroid * norm) per
-//                 element exactly as the reference decodes it (the scores are
-//                 the precision-critical part); V uses fp16 centroids with the
-//                 V norm folded into P.  QK^T and PV run on MFMA
-//                 16x16x32 f16 with the GQA group as the N=16 side, and keeps
-//                 an exp2-domain online softmax.  It writes (O_unnorm, m, l).
+//                 wave w owns KV head 8*blockIdx.y + w and its GQA group.  Two
+//                 kernels compute the same partials: decode_stream_kernel
+//                 (8 KV heads, 144-byte slots, one codebook for K and V;
+//                 pages stream into per-wave LDS rings by DMA, 64 tokens per
+//                 step) and decode_split_kernel (any head count and slot
+//                 width; 32 tokens per step loaded straight into registers).
+//                 Codes are dequantised through LDS tables indexed by code
+//                 byte, one table column per lane so reads do not conflict.
+//                 K and V are both rebuilt as fp16(centroid * norm) per
+//                 element, exactly as the reference decodes them
+//                 (compression.py:355-359).  QK^T and PV run on MFMA 16x16x32
+//                 f16 with the GQA group as the N=16 side, with an exp2-domain
+//                 online softmax.  It writes (O_unnorm, m, l) per split.
 //   3. combine:   merges the splits (attention.py:239-272), rounds O_rot to
 //                 fp16 (attention.py:93), applies R^T (compression.py:293-296)
 //                 and writes fp16 out.
 #include "cda_common.h"
 
 #include <type_traits>
+#include <utility>
 
 namespace cda {
 
@@ -36,12 +38,12 @@ typedef float floatx4 __attribute__((ext_vector_type(4)));
 constexpr int kWaves = 8;                 // KV heads per workgroup
 constexpr int kThreads = 64 * kWaves;
 constexpr int kChunk = 32;                // tokens per inner iteration (2 MFMA tiles)
-// Dequant tables in LDS (128 KiB), one 256-byte row per code byte e:
-//   K at [0, 64 KiB):      e*256 + c*8, fp32 centroid pair, 32 lane columns
-//   V at [64 KiB, 128 KiB): 65536 + e*256 + c*4, fp16 centroid pair, 64 columns
-// Lane l reads K column (l & 31) and V column l, so reads never conflict, and
-// the byte address is one v_perm of the code byte with a per-lane constant
-// (byte 2 of that constant carries the 64 KiB bit of the V table).
+// Dequant tables of decode_split_kernel in LDS (128 KiB), one 256-byte row per
+// code byte e holding the fp32 centroid pair (cb[e >> 4], cb[e & 15]) for 32
+// lane columns: K at [0, 64 KiB), V at [64 KiB, 128 KiB).  Lane l reads column
+// (l & 31), so reads never conflict, and the byte address is one v_perm of the
+// code byte with a per-lane constant (byte 2 of that constant carries the
+// 64 KiB bit of the V table).
 constexpr int kLutDwords = 2 * 256 * 64;
 constexpr float kLog2e = 1.4426950408889634f;
 
@@ -69,22 +71,12 @@ struct SplitParams {
     float scale_log2;           // softmax scale * log2(e)
 };
 
-__device__ __forceinline__ uint32_t pack_h2(float lo, float hi) {
-    uint32_t a = (uint32_t)__half_as_ushort(__float2half_rn(lo));
-    uint32_t b = (uint32_t)__half_as_ushort(__float2half_rn(hi));
-    return a | (b << 16);
-}
-
 __device__ __forceinline__ floatx4 mfma16(uint4 a, uint4 b, floatx4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, a),
                                                   __builtin_bit_cast(half8, b), c, 0, 0, 0);
 }
 
-// LDS table reads: byte address = code_byte * 256 + column offset.
-__device__ __forceinline__ uint32_t lut_at(const uint32_t *lut, uint32_t addr) {
-    return *reinterpret_cast<const uint32_t *>(reinterpret_cast<const char *>(lut) + addr);
-}
-
+// LDS table read: byte address = code_byte * 256 + column offset.
 __device__ __forceinline__ float2 lut2_at(const uint32_t *lut, uint32_t addr) {
     return *reinterpret_cast<const float2 *>(reinterpret_cast<const char *>(lut) + addr);
 }
@@ -95,6 +87,13 @@ __device__ __forceinline__ uint32_t cvt_pk_rn(float a, float b) {
     typedef _Float16 half2_ __attribute__((ext_vector_type(2)));
     const half2_ h = __builtin_convertvector(float2_{a, b}, half2_);
     return __builtin_bit_cast(uint32_t, h);
+}
+
+// max of three floats, NaN-propagating (v_maximum3_f32 on gfx950; no
+// canonicalisation moves).  Compiler-visible, so the MFMA-result read
+// hazards before it are handled by the compiler.
+__device__ __forceinline__ float max3f(float a, float b, float c) {
+    return __builtin_elementwise_maximum(__builtin_elementwise_maximum(a, b), c);
 }
 
 // Table address of code byte k of `w`: byte 0 <- col.byte0, byte 1 <- w.byte[k],
@@ -169,7 +168,7 @@ decode_split_kernel(SplitParams p) {
         for (int i = tid; i < kLutDwords / 2; i += kThreads) {
             const int e = i >> 6;
             lds[i] = __float_as_uint(cbs[0][(i & 1) ? (e & 15) : (e >> 4)]);
-            lds[kLutDwords / 2 + i] = pack_h2(cbs[1][e >> 4], cbs[1][e & 15]);
+            lds[kLutDwords / 2 + i] = __float_as_uint(cbs[1][(i & 1) ? (e & 15) : (e >> 4)]);
         }
         __syncthreads();
     }
@@ -210,7 +209,7 @@ decode_split_kernel(SplitParams p) {
     }
 
     const uint32_t colK = (uint32_t)(lane & 31) * 8u;
-    const uint32_t colV = 0x10000u | ((uint32_t)lane * 4u);
+    const uint32_t colV = 0x10000u | ((uint32_t)(lane & 31) * 8u);
     const int KB = kD / 2;
     LaneOffsets lo;
     lo.k = (uint32_t)(r16 * p.row_bytes + q4 * 16);
@@ -290,12 +289,12 @@ decode_split_kernel(SplitParams p) {
                 ev[2 * t + m2] = (wa & 0xF0F0F0F0u) | ((wb >> 4) & 0x0F0F0F0Fu);
                 od[2 * t + m2] = ((wa << 4) & 0xF0F0F0F0u) | (wb & 0x0F0F0F0Fu);
             }
-        uint4 vb[8];
+        float2 vc[32];
 #define CDA_V_TILE(K_, SRC_, J_)                                               \
-    vb[J_].x = lut_at(lds, lut_addr<K_>(SRC_[0], colV));                       \
-    vb[J_].y = lut_at(lds, lut_addr<K_>(SRC_[1], colV));                       \
-    vb[J_].z = lut_at(lds, lut_addr<K_>(SRC_[2], colV));                       \
-    vb[J_].w = lut_at(lds, lut_addr<K_>(SRC_[3], colV));
+    vc[4 * (J_) + 0] = lut2_at(lds, lut_addr<K_>(SRC_[0], colV));              \
+    vc[4 * (J_) + 1] = lut2_at(lds, lut_addr<K_>(SRC_[1], colV));              \
+    vc[4 * (J_) + 2] = lut2_at(lds, lut_addr<K_>(SRC_[2], colV));              \
+    vc[4 * (J_) + 3] = lut2_at(lds, lut_addr<K_>(SRC_[3], colV));
         CDA_V_TILE(0, ev, 0)
         CDA_V_TILE(0, od, 1)
         CDA_V_TILE(1, ev, 2)
@@ -315,8 +314,9 @@ decode_split_kernel(SplitParams p) {
                 raw[t][i] = sc[t][i];
                 if (MASK && c0 + 16 * t + 4 * q4 + i >= end) raw[t][i] = -INFINITY;
             }
-        float cmax = fmaxf(fmaxf(fmaxf(raw[0][0], raw[0][1]), fmaxf(raw[0][2], raw[0][3])),
-                           fmaxf(fmaxf(raw[1][0], raw[1][1]), fmaxf(raw[1][2], raw[1][3])));
+        float cmax = max3f(max3f(raw[0][0], raw[0][1], raw[0][2]),
+                           max3f(raw[0][3], raw[1][0], raw[1][1]),
+                           max3f(raw[1][2], raw[1][3], raw[1][3]));
         cmax = rows_max(cmax);
         const float m_new = fmaxf(m_run, cmax * p.scale_log2);
         const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);   // m_run = -inf -> 0
@@ -330,8 +330,8 @@ decode_split_kernel(SplitParams p) {
             for (int i = 0; i < 4; ++i) {
                 const float pr = __builtin_amdgcn_exp2f(fmaf(raw[t][i], p.scale_log2, -m_new));
                 psum += pr;
-                // A masked token weighs 0 (its V norm may be garbage).
-                pv[t][i] = (MASK && c0 + 16 * t + 4 * q4 + i >= end) ? 0.0f : pr * c.nv[t][i];
+                // A masked token weighs 0 (its V may be garbage).
+                pv[t][i] = (MASK && c0 + 16 * t + 4 * q4 + i >= end) ? 0.0f : pr;
             }
         l_run = fmaf(l_run, alpha, psum);
         uint4 pa;
@@ -361,8 +361,23 @@ decode_split_kernel(SplitParams p) {
 #pragma unroll
                 for (int i = 0; i < 4; ++i) acc_o[j][i] *= f[i];
         }
+        // V rebuilt exactly as the reference decodes it: fp16(centroid * norm)
+        // per element; a masked token's V is zeroed (0 * garbage could be NaN).
+        float nva[2][4];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) acc_o[j] = mfma16(pa, vb[j], acc_o[j]);
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                nva[t][i] = (MASK && c0 + 16 * t + 4 * q4 + i >= end) ? 0.0f : c.nv[t][i];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            uint4 vb;
+            vb.x = cvt_pk_rn(vc[4 * j + 0].x * nva[0][0], vc[4 * j + 0].y * nva[0][1]);
+            vb.y = cvt_pk_rn(vc[4 * j + 1].x * nva[0][2], vc[4 * j + 1].y * nva[0][3]);
+            vb.z = cvt_pk_rn(vc[4 * j + 2].x * nva[1][0], vc[4 * j + 2].y * nva[1][1]);
+            vb.w = cvt_pk_rn(vc[4 * j + 3].x * nva[1][2], vc[4 * j + 3].y * nva[1][3]);
+            acc_o[j] = mfma16(pa, vb, acc_o[j]);
+        }
     };
 
     // ---- main loop over the full 32-token chunks; loads run one chunk
@@ -425,34 +440,40 @@ decode_split_kernel(SplitParams p) {
 }
 
 // ---------------------------------------------------------------------------
-// Page-streaming variant for the common cache shape: 8 KV heads x 144-byte
-// slots, a block size that is a multiple of 16 and one codebook for K and V.
+// Page-streaming split kernel for the common cache shape: 8 KV heads x
+// 144-byte slots, a block size that is a multiple of 16 and one codebook for
+// K and V.
 //
 // Wave h (one per KV head) streams its head's share of each 16-token page
-// (16 x 144 B = 2304 B) into a private 5-page LDS ring with the gfx950
+// (16 x 144 B = 2304 B) into a private 4-page LDS ring with the gfx950
 // direct-to-LDS DMA (buffer_load_dwordx4 ... lds): three instructions per page
 // (K codes, V codes, norms), each lane fetching one 16-byte piece.  The waves
-// never wait for each other: each one waits on its own DMA counter only, reads
-// a chunk of two pages into registers, refills the two slots at once and
-// computes while three pages are in flight (more in flight measured slower).  Within a page the pieces are laid
-// out so that every read below is free of LDS bank conflicts:
+// never wait for each other: each one waits on its own DMA counter only.  A
+// step takes a chunk of four pages (64 tokens): wait for the chunk's DMAs,
+// read the four pages into registers, refill the four slots with the next
+// chunk (in flight while this one computes), then QK^T on the four pages
+// (independent MFMA chains), one online-softmax update over the 64 tokens and
+// PV over two page pairs.  Page k of a chunk lives in ring slot k, so every
+// ring offset is an immediate.  Within a page the pieces are laid out so that
+// every read is free of LDS bank conflicts:
 //   [0, 1024)     K codes: piece 16*c + t = token t, 16-byte column c (0..3)
 //   [1024, 2048)  V codes: token t's 64 bytes at 64 * vslot(t)
 //   [2048, 2304)  norms:   token t's (Kn, Vn, pad) at 16 * t
 // One dequant table serves K and V: row e (256 B) holds (cb[e >> 4],
 // cb[e & 15]) in fp32 for 32 lane columns, read with one ds_read_b64 per code
-// byte; K is rebuilt as fp16(centroid * norm), V rounds the centroid to fp16.
+// byte.
 // ---------------------------------------------------------------------------
 
 constexpr int kStreamRowBytes = 8 * 144;
 constexpr int kPageBytes = 16 * kStreamRowBytes;          // one 16-token page, all heads
 constexpr int kHeadPage = 16 * 144;                        // one head's share: 2304 B
-constexpr int kRingPages = 3;
+#define CDA_INLINE __attribute__((always_inline))
+
+template <int N>
+using IC = std::integral_constant<int, N>;
+
 constexpr int kLut2Bytes = 256 * 64 * 4;                   // 64 KiB
 constexpr int kStreamMaxPages = 1024;                      // page rows staged in LDS
-constexpr int kRingOff = kLut2Bytes;
-constexpr int kStreamPidOff = kRingOff + kWaves * kRingPages * kHeadPage;
-constexpr int kStreamLds = kStreamPidOff + kStreamMaxPages * 4;   // 161792 B
 
 typedef unsigned v4u32 __attribute__((ext_vector_type(4)));
 
@@ -462,7 +483,7 @@ typedef unsigned v4u32 __attribute__((ext_vector_type(4)));
 // serialise the ring); completion is ordered by the explicit vmcnt waits.
 __device__ __forceinline__ void dma_page_chunk(v4u32 rsrc, uint32_t voff, uint32_t lds_base) {
     asm volatile("s_mov_b32 m0, %2\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds"
-                 :: "v"(voff), "s"(rsrc), "s"(lds_base) : "memory");
+                 :: "v"(voff), "s"(rsrc), "s"(lds_base) : "memory", "m0");
 }
 
 __device__ __forceinline__ uint32_t lds_u32addr(const void *p) {
@@ -478,6 +499,11 @@ __device__ __forceinline__ uint32_t lds_b32(const uint8_t *base, uint32_t off) {
 __host__ __device__ constexpr int vslot(int t) { return (t & 12) | ((t + (t >> 2)) & 3); }
 __host__ __device__ constexpr int vslot_inv(int s) { return (s & 12) | ((s - (s >> 2)) & 3); }
 
+constexpr int kStreamPages = 4;
+constexpr int kStreamRingOff = kLut2Bytes;
+constexpr int kStreamPidOff = kStreamRingOff + kWaves * kStreamPages * kHeadPage;
+constexpr int kStreamLds = kStreamPidOff + kStreamMaxPages * 4;           // 143360 B
+
 template <int GS>
 __global__ void __launch_bounds__(kThreads, 1)
 decode_stream_kernel(SplitParams p) {
@@ -488,7 +514,7 @@ decode_stream_kernel(SplitParams p) {
     const int tid = threadIdx.x;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int lane = tid & 63;
-    const int h = wave;                       // this variant has exactly 8 KV heads
+    const int h = wave;
     const int r16 = lane & 15;
     const int q4 = lane >> 4;
 
@@ -506,19 +532,15 @@ decode_stream_kernel(SplitParams p) {
         return;
     }
 
-    // ---- DMA sources (offsets in the head's share of a page) of this lane's
-    // piece in each of the three instructions; see the layout above.
     uint32_t src[3];
     src[0] = (uint32_t)((lane & 15) * kStreamRowBytes + (lane >> 4) * 16);
     src[1] = (uint32_t)(vslot_inv(lane >> 2) * kStreamRowBytes + 64 + (lane & 3) * 16);
     src[2] = (uint32_t)((lane & 15) * kStreamRowBytes + 128);   // lanes 0..15 only
 
     const int bs = p.block_size;
-    const int npages = (end - start + 15) >> 4;     // <= kStreamMaxPages (host check)
-    const uint32_t ring_w =
-        __builtin_amdgcn_readfirstlane(lds_u32addr(smem)) + kRingOff + wave * (kRingPages * kHeadPage);
-    // First cache row of each page of the split, staged in LDS: a block-table
-    // read per page would stall the wave on memory latency before each DMA.
+    const int npages = (end - start + 15) >> 4;
+    const uint32_t ring_w = __builtin_amdgcn_readfirstlane(lds_u32addr(smem)) + kStreamRingOff +
+                            wave * (kStreamPages * kHeadPage);
     int32_t *page_row = reinterpret_cast<int32_t *>(smem + kStreamPidOff);
     {
         const int32_t *bt = p.block_table + (int64_t)b * p.bt_stride;
@@ -528,19 +550,18 @@ decode_stream_kernel(SplitParams p) {
         }
     }
     const uint8_t *kv_h = p.kv + h * 144;
-    auto issue = [&](int t) {
+    // DMA of page t into ring slot k.
+    auto issue = [&](int t, int k) CDA_INLINE {
         const int64_t row0 = __builtin_amdgcn_readfirstlane(page_row[t]);
         const uint64_t base = (uint64_t)(kv_h + row0 * kStreamRowBytes);
-        const v4u32 r = {(uint32_t)base, (uint32_t)(base >> 32) & 0xFFFFu,
+        const v4u32 r = {(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)base),
+                         (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(base >> 32) & 0xFFFFu),
                          (uint32_t)(kPageBytes - h * 144), 0x00020000u};
-        const uint32_t sb = ring_w + (uint32_t)(t % kRingPages) * kHeadPage;
+        const uint32_t sb = ring_w + (uint32_t)k * kHeadPage;
         dma_page_chunk(r, src[0], sb);
         dma_page_chunk(r, src[1], sb + 1024);
         if (lane < 16) dma_page_chunk(r, src[2], sb + 2048);
     };
-    // ---- query operand (B of QK^T): column g = r16, k slots = dims 32*q4+8*s+j.
-    // Columns g >= GS repeat query g % GS: their scores are never used (no
-    // alpha, m or output is read from them) and stay finite.
     uint4 qb[4];
     {
         const uint16_t *qg =
@@ -548,8 +569,6 @@ decode_stream_kernel(SplitParams p) {
 #pragma unroll
         for (int s = 0; s < 4; ++s) qb[s] = *reinterpret_cast<const uint4 *>(qg + 8 * s);
     }
-
-    // ---- dequant table.
     {
         uint32_t *lut = reinterpret_cast<uint32_t *>(smem);
         for (int i = tid; i < kLut2Bytes / 4; i += kThreads) {
@@ -558,19 +577,13 @@ decode_stream_kernel(SplitParams p) {
         }
     }
     __syncthreads();
-    // Every vector load the compiler issued above has landed: from here on the
-    // vector-memory counter tracks this wave's DMAs only.
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
-    // Ring prologue: pages 0..2 (as many as exist).  Page t lives in slot t % 3.
 #pragma unroll
-    for (int t = 0; t < kRingPages; ++t)
-        if (t < npages) issue(t);
+    for (int k = 0; k < kStreamPages; ++k)
+        if (k < npages) issue(k, k);
 
-    // Per-lane read offsets inside a page share.
-    // Per-lane read offsets inside this wave's ring (slot 0); the slot adds
-    // a compile-time immediate.
-    const uint32_t rb0 = (uint32_t)(kRingOff + wave * (kRingPages * kHeadPage));
+    const uint32_t rb0 = (uint32_t)(kStreamRingOff + wave * (kStreamPages * kHeadPage));
     const uint32_t oK = rb0 + (uint32_t)lane * 16u;
     const uint32_t oNK = rb0 + 2048u + 16u * r16;
     uint32_t oV[4], oNV[4];
@@ -588,16 +601,14 @@ decode_stream_kernel(SplitParams p) {
     float m_run = -INFINITY;
     float l_run = 0.0f;
 
-    // (cb[hi], cb[lo]) of code byte k of w: one 8-byte read.
 #define CDA_PAIR(K_, W_) (*reinterpret_cast<const float2 *>(lutb + lut_addr<K_>(W_, col)))
-
     struct PageRegs {
-        uint4 kq;          // K codes: token r16, dims [32*q4, 32*q4+32)
-        float nk;          // K norm of token r16
-        uint32_t vw[4];    // V codes: token 4*q4+k, dims [8*r16, 8*r16+8)
-        float nv[4];       // V norm of token 4*q4+k
+        uint4 kq;
+        float nk;
+        uint32_t vw[4];
+        float nv[4];
     };
-    auto read_page = [&](PageRegs &r, auto slot) {
+    auto read_page = [&](PageRegs &r, auto slot) CDA_INLINE {
         constexpr uint32_t so = decltype(slot)::value * kHeadPage;
         r.kq = *reinterpret_cast<const uint4 *>(smem + oK + so);
         r.nk = __uint_as_float(lds_b32(smem + so, oNK));
@@ -607,9 +618,7 @@ decode_stream_kernel(SplitParams p) {
             r.nv[k] = __uint_as_float(lds_b32(smem + so, oNV[k]));
         }
     };
-
-    // ---- scores of one page: its 16 tokens (rows) x the queries (columns).
-    auto page_scores = [&](const PageRegs &r) -> floatx4 {
+    auto page_scores = [&](const PageRegs &r) CDA_INLINE -> floatx4 {
         const uint32_t w[4] = {r.kq.x, r.kq.y, r.kq.z, r.kq.w};
         float2 cv[16];
 #pragma unroll
@@ -632,23 +641,15 @@ decode_stream_kernel(SplitParams p) {
         }
         return acc;
     };
-
-    // ---- softmax + PV over a chunk of two pages; tokens at or past `end`
-    // weigh 0.
-    auto finish_chunk = [&](floatx4 sc0, floatx4 sc1, const PageRegs &r0, const PageRegs &r1,
-                            int c0, auto masked) {
-        constexpr bool MASK = decltype(masked)::value;
-        // V operand (B of PV): column r16 of tile j holds dim 8*r16 + j; k slot
-        // pairs (2p, 2p+1) = tokens (4*q4 + 2*(p%2), +1) of page p/2.  Pair two
-        // tokens' nibbles of one dim into one byte, so one table read gives
-        // both values.
+    // O += P V over pages ra, rb (k slots as in decode_stream_kernel).
+    auto pv_pair = [&](const uint4 &pa, const PageRegs &ra, const PageRegs &rb) CDA_INLINE {
         uint32_t ev[4], od[4];
 #pragma unroll
         for (int m2 = 0; m2 < 2; ++m2) {
-            ev[m2] = (r0.vw[2 * m2] & 0xF0F0F0F0u) | ((r0.vw[2 * m2 + 1] >> 4) & 0x0F0F0F0Fu);
-            od[m2] = ((r0.vw[2 * m2] << 4) & 0xF0F0F0F0u) | (r0.vw[2 * m2 + 1] & 0x0F0F0F0Fu);
-            ev[2 + m2] = (r1.vw[2 * m2] & 0xF0F0F0F0u) | ((r1.vw[2 * m2 + 1] >> 4) & 0x0F0F0F0Fu);
-            od[2 + m2] = ((r1.vw[2 * m2] << 4) & 0xF0F0F0F0u) | (r1.vw[2 * m2 + 1] & 0x0F0F0F0Fu);
+            ev[m2] = (ra.vw[2 * m2] & 0xF0F0F0F0u) | ((ra.vw[2 * m2 + 1] >> 4) & 0x0F0F0F0Fu);
+            od[m2] = ((ra.vw[2 * m2] << 4) & 0xF0F0F0F0u) | (ra.vw[2 * m2 + 1] & 0x0F0F0F0Fu);
+            ev[2 + m2] = (rb.vw[2 * m2] & 0xF0F0F0F0u) | ((rb.vw[2 * m2 + 1] >> 4) & 0x0F0F0F0Fu);
+            od[2 + m2] = ((rb.vw[2 * m2] << 4) & 0xF0F0F0F0u) | (rb.vw[2 * m2 + 1] & 0x0F0F0F0Fu);
         }
         float2 vc[32];
 #define CDA_V_TILE(K_, SRC_, J_)                                               \
@@ -665,38 +666,94 @@ decode_stream_kernel(SplitParams p) {
         CDA_V_TILE(3, ev, 6)
         CDA_V_TILE(3, od, 7)
 #undef CDA_V_TILE
-        float raw[2][4];
+        // V rebuilt exactly as the reference decodes it: fp16(centroid * norm)
+        // per element (k slot pairs are two tokens of one dim).
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            raw[0][i] = sc0[i];
-            raw[1][i] = sc1[i];
-            if (MASK && c0 + 4 * q4 + i >= end) raw[0][i] = -INFINITY;
-            if (MASK && c0 + 16 + 4 * q4 + i >= end) raw[1][i] = -INFINITY;
+        for (int j = 0; j < 8; ++j) {
+            uint4 vb;
+            vb.x = cvt_pk_rn(vc[4 * j + 0].x * ra.nv[0], vc[4 * j + 0].y * ra.nv[1]);
+            vb.y = cvt_pk_rn(vc[4 * j + 1].x * ra.nv[2], vc[4 * j + 1].y * ra.nv[3]);
+            vb.z = cvt_pk_rn(vc[4 * j + 2].x * rb.nv[0], vc[4 * j + 2].y * rb.nv[1]);
+            vb.w = cvt_pk_rn(vc[4 * j + 3].x * rb.nv[2], vc[4 * j + 3].y * rb.nv[3]);
+            acc_o[j] = mfma16(pa, vb, acc_o[j]);
         }
-        float cmax = fmaxf(fmaxf(fmaxf(raw[0][0], raw[0][1]), fmaxf(raw[0][2], raw[0][3])),
-                           fmaxf(fmaxf(raw[1][0], raw[1][1]), fmaxf(raw[1][2], raw[1][3])));
-        cmax = rows_max(cmax);
-        const float m_new = fmaxf(m_run, cmax * p.scale_log2);
-        const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);   // m_run = -inf -> 0
-        m_run = m_new;
-        float pv[2][4];
-        float psum = 0.0f;
+    };
+
+    // ---- one chunk of four pages starting at page 4c (token c0).
+    auto step = [&](int c, auto masked) CDA_INLINE {
+        constexpr bool MASK = decltype(masked)::value;
+        const int c0 = start + 64 * c;
+        const int p0 = 4 * c;
+        __builtin_amdgcn_s_waitcnt(0x0F70);        // this chunk's DMAs (the only ones in flight)
+        asm volatile("" ::: "memory");
+        PageRegs r[4];
+        read_page(r[0], IC<0>{});
+        if (!MASK || p0 + 1 < npages) read_page(r[1], IC<1>{});
+        if (!MASK || p0 + 2 < npages) read_page(r[2], IC<2>{});
+        if (!MASK || p0 + 3 < npages) read_page(r[3], IC<3>{});
+        if (MASK) {
+            // Pages past the split are not read: zero codes and norms (their
+            // tokens are masked out below).
 #pragma unroll
-        for (int t = 0; t < 2; ++t)
+            for (int k = 1; k < 4; ++k)
+                if (p0 + k >= npages) {
+                    r[k].kq = make_uint4(0, 0, 0, 0);
+                    r[k].nk = 0.0f;
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        r[k].vw[i] = 0u;
+                        r[k].nv[i] = 0.0f;
+                    }
+                }
+        }
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        if (!MASK) {
+            // Refill the four slots with the next chunk.
+            const int n0 = p0 + 4;
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+                if (n0 + k < npages) issue(n0 + k, k);
+        }
+        floatx4 sc[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) sc[k] = page_scores(r[k]);
+        float raw[4][4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const float pr = __builtin_amdgcn_exp2f(fmaf(raw[t][i], p.scale_log2, -m_new));
+                raw[k][i] = sc[k][i];
+                if (MASK && c0 + 16 * k + 4 * q4 + i >= end) raw[k][i] = -INFINITY;
+            }
+        float cmax = max3f(max3f(raw[0][0], raw[0][1], raw[0][2]),
+                           max3f(raw[0][3], raw[1][0], raw[1][1]),
+                           max3f(raw[1][2], raw[1][3], raw[2][0]));
+        cmax = max3f(cmax, max3f(raw[2][1], raw[2][2], raw[2][3]),
+                     max3f(raw[3][0], raw[3][1], max3f(raw[3][2], raw[3][3], raw[3][3])));
+        cmax = rows_max(cmax);
+        const float m_new = fmaxf(m_run, cmax * p.scale_log2);
+        const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+        m_run = m_new;
+        float pv[4][4];
+        float psum = 0.0f;
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float pr = __builtin_amdgcn_exp2f(fmaf(raw[k][i], p.scale_log2, -m_new));
                 psum += pr;
-                // A masked token weighs 0 (its ring slot may hold stale data).
-                const float nvv = t ? r1.nv[i] : r0.nv[i];
-                pv[t][i] = (MASK && c0 + 16 * t + 4 * q4 + i >= end) ? 0.0f : pr * nvv;
+                pv[k][i] = (MASK && c0 + 16 * k + 4 * q4 + i >= end) ? 0.0f : pr;
             }
         l_run = fmaf(l_run, alpha, psum);
-        uint4 pa;
-        pa.x = cvt_pk_rn(pv[0][0], pv[0][1]);
-        pa.y = cvt_pk_rn(pv[0][2], pv[0][3]);
-        pa.z = cvt_pk_rn(pv[1][0], pv[1][1]);
-        pa.w = cvt_pk_rn(pv[1][2], pv[1][3]);
+        uint4 pa0, pa1;
+        pa0.x = cvt_pk_rn(pv[0][0], pv[0][1]);
+        pa0.y = cvt_pk_rn(pv[0][2], pv[0][3]);
+        pa0.z = cvt_pk_rn(pv[1][0], pv[1][1]);
+        pa0.w = cvt_pk_rn(pv[1][2], pv[1][3]);
+        pa1.x = cvt_pk_rn(pv[2][0], pv[2][1]);
+        pa1.y = cvt_pk_rn(pv[2][2], pv[2][3]);
+        pa1.z = cvt_pk_rn(pv[3][0], pv[3][1]);
+        pa1.w = cvt_pk_rn(pv[3][2], pv[3][3]);
         float al[GS];
         bool moved = false;
 #pragma unroll
@@ -718,76 +775,23 @@ decode_stream_kernel(SplitParams p) {
 #pragma unroll
                 for (int i = 0; i < 4; ++i) acc_o[j][i] *= f[i];
         }
+        if (MASK) {
+            // A masked token's V is zeroed: its slot may hold garbage norms.
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            uint4 vb;
-            vb.x = cvt_pk_rn(vc[4 * j + 0].x, vc[4 * j + 0].y);
-            vb.y = cvt_pk_rn(vc[4 * j + 1].x, vc[4 * j + 1].y);
-            vb.z = cvt_pk_rn(vc[4 * j + 2].x, vc[4 * j + 2].y);
-            vb.w = cvt_pk_rn(vc[4 * j + 3].x, vc[4 * j + 3].y);
-            acc_o[j] = mfma16(pa, vb, acc_o[j]);
+            for (int k = 0; k < 4; ++k)
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    if (c0 + 16 * k + 4 * q4 + i >= end) r[k].nv[i] = 0.0f;
         }
+        pv_pair(pa0, r[0], r[1]);
+        pv_pair(pa1, r[2], r[3]);
     };
 #undef CDA_PAIR
 
-    // ---- main loop over chunks of two pages.  Chunk i: wait for this wave's
-    // DMAs of pages <= 2i+1, read both pages into registers, refill their
-    // slots with pages 2i+5, 2i+6, then compute.
-    auto step = [&](int i, auto sa, auto sb, auto masked) {
-        // DMAs allowed in flight = 3 per page issued beyond page 2i+1 (<= 3
-        // pages); vmcnt takes an immediate, hence the case split.
-        const int ahead = max(min(npages, 2 * i + kRingPages) - (2 * i + 2), 0);
-        switch (ahead) {
-        case 3: __builtin_amdgcn_s_waitcnt(0x0F70 | 9); break;
-        case 2: __builtin_amdgcn_s_waitcnt(0x0F70 | 6); break;
-        case 1: __builtin_amdgcn_s_waitcnt(0x0F70 | 3); break;
-        default: __builtin_amdgcn_s_waitcnt(0x0F70); break;
-        }
-        asm volatile("" ::: "memory");
-        PageRegs r0, r1;
-        read_page(r0, sa);
-        if (2 * i + 1 < npages) {
-            read_page(r1, sb);
-        } else {
-            // A chunk of one page: the second half is past `end`, masked out.
-            r1.kq = make_uint4(0, 0, 0, 0);
-            r1.nk = 0.0f;
-#pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                r1.vw[k] = 0u;
-                r1.nv[k] = 0.0f;
-            }
-        }
-        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-        if (2 * i + kRingPages < npages) issue(2 * i + kRingPages);
-        if (2 * i + kRingPages + 1 < npages) issue(2 * i + kRingPages + 1);
-        const floatx4 sc0 = page_scores(r0);
-        const floatx4 sc1 = page_scores(r1);
-        finish_chunk(sc0, sc1, r0, r1, start + 32 * i, masked);
-    };
-    // Full chunks first (no masking in the loop body), then the partial one.
-    // Chunk i reads slots (2i) % 3 and (2i+1) % 3: the slot pattern repeats
-    // every three chunks, so the loop is unrolled by three.
-    using S0 = std::integral_constant<int, 0>;
-    using S1 = std::integral_constant<int, 1>;
-    using S2 = std::integral_constant<int, 2>;
-    const int nchunks = (npages + 1) >> 1;
-    const int nfull = (end - start) >> 5;
-    int i = 0;
-    for (; i + 3 <= nfull; i += 3) {
-        step(i, S0{}, S1{}, std::false_type{});
-        step(i + 1, S2{}, S0{}, std::false_type{});
-        step(i + 2, S1{}, S2{}, std::false_type{});
-    }
-    for (; i < nfull; ++i) {
-        if (i % 3 == 0) step(i, S0{}, S1{}, std::false_type{});
-        else step(i, S2{}, S0{}, std::false_type{});      // i % 3 == 1 (at most two left)
-    }
-    if (nfull < nchunks) {
-        if (nfull % 3 == 0) step(nfull, S0{}, S1{}, std::true_type{});
-        else if (nfull % 3 == 1) step(nfull, S2{}, S0{}, std::true_type{});
-        else step(nfull, S1{}, S2{}, std::true_type{});
-    }
+    const int nchunks = (npages + 3) >> 2;
+    const int nfull = (end - start) >> 6;
+    for (int c = 0; c < nfull; ++c) step(c, std::false_type{});
+    if (nfull < nchunks) step(nfull, std::true_type{});
 
     const float l = rows_sum(l_run);
     if (q4 == 0 && r16 < GS) {

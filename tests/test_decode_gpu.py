@@ -89,6 +89,22 @@ def test_decode_general_kernel_matches_checker(gpu, name, seq_lens, gs, bs, tile
     check(streamed, general, tol=1e-3)
 
 
+@pytest.mark.parametrize("seed,seq_lens", [(6, [65, 64, 63, 1]), (80, [1, 2, 3, 5, 9, 17])])
+def test_decode_short_sequences(gpu, seed, seq_lens):
+    """Few keys, so outputs reach |x| ~ 3 where one fp16 ulp is ~2e-3: V must
+    be rebuilt as fp16(centroid * norm) per element, as the reference decodes
+    it (a norm folded into P put these cases 2 ulps off).  Both kernels."""
+    from sub0_amd import _native
+    print(f"[decode-short] seed={seed} seq_lens={seq_lens}", flush=True)
+    case = make_decode_case(seed, seq_lens, H_kv=8, gs=4, fill=0xFF)
+    check(run_gpu_decode(case, gpu, gs=4), case.expected)
+    _native.set_stream_kernel(False)
+    try:
+        check(run_gpu_decode(case, gpu, gs=4), case.expected)
+    finally:
+        _native.set_stream_kernel(True)
+
+
 def test_decode_separate_equal_codebooks(gpu):
     """cb_K and cb_V as separate tensors with equal values (the reference
     passes one Compressor's codebook each)."""
