@@ -8,9 +8,8 @@
   16-level (K4V4) and 4-level (K2V2) codebooks.
 
 Argument checks and error types follow the reference.  The split size
-(``_choose_tile_n``) is MI355X's own policy: it targets about four
-512-thread workgroups per CU (256 CUs) instead of the reference's
-2-blocks-per-SM rule, and it is what the kernel plans with when called
+(``_choose_tile_n``) is MI355X's own policy: it targets one 512-thread
+workgroup per CU (256 CUs) instead of the reference's 2-blocks-per-SM rule, and it is what the kernel plans with when called
 through these wrappers.
 """
 from __future__ import annotations
@@ -40,8 +39,9 @@ def _choose_tile_n(past_len: int, *, B: int = 1, H_q: int = 32, device_idx: int 
     """Context tokens per split-K partition (reference ``wrappers.py:41-76``).
 
     MI355X policy (``cda_decode_plan`` in the HIP library): one workgroup
-    covers 8 KV heads of one sequence; aim for ~4 workgroups per CU, at least
-    64 tokens and at most 512 partitions per sequence, rounded to 32 tokens.
+    covers 8 KV heads of one sequence; aim for one workgroup per CU, at least
+    64 and at most 16384 tokens and at most 512 partitions per sequence,
+    rounded to 32 tokens.
     ``device_idx`` is accepted for signature parity.
     """
     H_kv = max(1, H_q // group_size)

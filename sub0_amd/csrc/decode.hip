@@ -995,13 +995,19 @@ extern "C" int cda_decode_plan(int B, int H_q, int H_kv, int max_seq_len, int ti
     if (tile_n > 0) {
         tn = (tile_n + kChunk - 1) / kChunk * kChunk;
     } else {
-        // Aim for ~4 workgroups per CU, splits of at least 64 tokens and at
-        // most 512 splits per sequence.
+        // One workgroup per CU (the split kernels hold one per CU: their LDS
+        // tables are 128-143 KiB), so every split runs in a single round and
+        // the per-workgroup set-up is paid once per CU; splits of at least 64
+        // tokens, at most 16384 (the streaming kernel's page-row table) and at
+        // most 512 per sequence.  Measured at B=32, N=64K: 8 splits 527 us,
+        // 16: 530, 32: 545, 64: 578.
         const int hg = (H_kv + kWaves - 1) / kWaves;
-        const int target = 4 * num_cus();
+        const int target = num_cus();
         int splits = (target + B * hg - 1) / (B * hg);
         const int max_by_len = (n + 63) / 64;
         if (splits > max_by_len) splits = max_by_len;
+        const int min_by_len = (n + 16 * kStreamMaxPages - 1) / (16 * kStreamMaxPages);
+        if (splits < min_by_len) splits = min_by_len;
         if (splits > 512) splits = 512;
         if (splits < 1) splits = 1;
         tn = (n + splits - 1) / splits;
