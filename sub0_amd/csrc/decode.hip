@@ -69,6 +69,7 @@ struct SplitParams {
     int tile_n;
     int n_splits;
     float scale_log2;           // softmax scale * log2(e)
+    int levels;                 // codebook levels: 16 (4-bit codes) or 4 (2-bit codes)
 };
 
 __device__ __forceinline__ floatx4 mfma16(uint4 a, uint4 b, floatx4 c) {
@@ -139,17 +140,39 @@ struct LaneOffsets {
     uint32_t k, nk, v[4], nv[4];
 };
 
+// Two bytes of 2-bit codes (pack_2bit: dim 4j at bits 7:6 of byte j,
+// compression.py:382-386) -> four bytes in the 4-bit layout (dim 2k in the
+// high nibble of byte k), so both code widths share the 4-bit tables.
+__device__ __forceinline__ uint32_t widen_2bit(uint32_t x) {
+    const uint32_t y = (x & 0xFFu) | ((x & 0xFF00u) << 8);
+    return ((y >> 2) & 0x00300030u) | ((y >> 4) & 0x00030003u) | ((y << 10) & 0x30003000u) |
+           ((y << 8) & 0x03000300u);
+}
+
+// One 16-token tile of a chunk.  L = 16: 16 K bytes and 4 V bytes per lane;
+// L = 4: 8 and 2, widened to the 4-bit layout.
+template <int L>
 __device__ __forceinline__ void load_tile(Chunk &c, int t, rsrc_t r, const LaneOffsets &o) {
-    c.kq[t] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, o.k, 0, 0));
+    if constexpr (L == 16) {
+        c.kq[t] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, o.k, 0, 0));
+    } else {
+        typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
+        const u32x2 k2 = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(r, o.k, 0, 0));
+        c.kq[t] = make_uint4(widen_2bit(k2.x & 0xFFFFu), widen_2bit(k2.x >> 16),
+                             widen_2bit(k2.y & 0xFFFFu), widen_2bit(k2.y >> 16));
+    }
     c.nk[t] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, o.nk, 0, 0));
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        c.vw[t][i] = __builtin_amdgcn_raw_buffer_load_b32(r, o.v[i], 0, 0);
+        if constexpr (L == 16)
+            c.vw[t][i] = __builtin_amdgcn_raw_buffer_load_b32(r, o.v[i], 0, 0);
+        else
+            c.vw[t][i] = widen_2bit(__builtin_amdgcn_raw_buffer_load_b16(r, o.v[i], 0, 0));
         c.nv[t][i] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, o.nv[i], 0, 0));
     }
 }
 
-template <int GS>
+template <int GS, int L>
 __global__ void __launch_bounds__(kThreads, 1)
 decode_split_kernel(SplitParams p) {
     __shared__ __align__(16) uint32_t lds[kLutDwords];
@@ -163,7 +186,12 @@ decode_split_kernel(SplitParams p) {
     // decode does.
     {
         __shared__ float cbs[2][16];
-        if (tid < 32) cbs[tid >> 4][tid & 15] = (tid < 16) ? p.cb_k[tid] : p.cb_v[tid - 16];
+        // Entries past the codebook are never indexed (widened 2-bit codes
+        // stay below 4); they are set to 0 rather than read out of bounds.
+        if (tid < 32) {
+            const int e = tid & 15;
+            cbs[tid >> 4][e] = (e < L) ? ((tid < 16) ? p.cb_k[e] : p.cb_v[e]) : 0.0f;
+        }
         __syncthreads();
         for (int i = tid; i < kLutDwords / 2; i += kThreads) {
             const int e = i >> 6;
@@ -210,13 +238,13 @@ decode_split_kernel(SplitParams p) {
 
     const uint32_t colK = (uint32_t)(lane & 31) * 8u;
     const uint32_t colV = 0x10000u | ((uint32_t)(lane & 31) * 8u);
-    const int KB = kD / 2;
+    constexpr int KB = (L == 16) ? kD / 2 : kD / 4;     // code bytes per role
     LaneOffsets lo;
-    lo.k = (uint32_t)(r16 * p.row_bytes + q4 * 16);
+    lo.k = (uint32_t)(r16 * p.row_bytes + q4 * (KB / 4));
     lo.nk = (uint32_t)(r16 * p.row_bytes + 2 * KB);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        lo.v[i] = (uint32_t)((4 * q4 + i) * p.row_bytes + KB + 4 * r16);
+        lo.v[i] = (uint32_t)((4 * q4 + i) * p.row_bytes + KB + (KB / 16) * r16);
         lo.nv[i] = (uint32_t)((4 * q4 + i) * p.row_bytes + 2 * KB + 4);
     }
     const int32_t *bt = p.block_table + (int64_t)b * p.bt_stride;
@@ -234,8 +262,8 @@ decode_split_kernel(SplitParams p) {
     auto load_chunk = [&](Chunk &c, int c0) {
         const rsrc_t r0 = tile_res(c0);
         const rsrc_t r1 = (c0 + 16 < end) ? tile_res(c0 + 16) : r0;
-        load_tile(c, 0, r0, lo);
-        load_tile(c, 1, r1, lo);
+        load_tile<L>(c, 0, r0, lo);
+        load_tile<L>(c, 1, r1, lo);
     };
 
     floatx4 acc_o[8];
@@ -1042,10 +1070,12 @@ extern "C" int cda_decode_full_hmma_v3(const void *q, const void *kv_cache, int6
                 "cda_decode_full_hmma_v3: group_size must be 4 or 8");
     CDA_REQUIRE(H_q == H_kv * group_size,
                 "cda_decode_full_hmma_v3: H_q must equal H_kv * group_size");
-    CDA_REQUIRE(levels == 16, "cda_decode_full_hmma_v3: the decode kernel reads K4V4 caches "
-                              "(16-level codebooks)");
-    CDA_REQUIRE(slot_bytes >= 2 * (kD / 2) + 8 && slot_bytes % 16 == 0,
-                "cda_decode_full_hmma_v3: slot_bytes must be >= 136 and a multiple of 16");
+    CDA_REQUIRE(levels == 16 || levels == 4,
+                "cda_decode_full_hmma_v3: codebooks must have 16 levels (K4V4) or 4 (K2V2)");
+    const int code_bytes = (levels == 16) ? kD / 2 : kD / 4;
+    CDA_REQUIRE(slot_bytes >= 2 * code_bytes + 8 && slot_bytes % 16 == 0,
+                "cda_decode_full_hmma_v3: slot_bytes must hold both code fields and the two "
+                "norms (>= 136 for K4V4, >= 72 for K2V2) and be a multiple of 16");
     CDA_REQUIRE(block_size > 0 && block_size % 16 == 0,
                 "cda_decode_full_hmma_v3: block_size must be a positive multiple of 16");
     CDA_REQUIRE(max_seq_len >= 0 && bt_stride > 0,
@@ -1090,11 +1120,13 @@ extern "C" int cda_decode_full_hmma_v3(const void *q, const void *kv_cache, int6
     p.tile_n = tn;
     p.n_splits = ns;
     p.scale_log2 = scale * kLog2e;
+    p.levels = levels;
     dim3 grid(ns, (H_kv + kWaves - 1) / kWaves, B);
     // The page-streaming kernel covers 8 KV heads x 144-byte slots with one
     // codebook for K and V (passed as the same pointer) and splits of at most
     // 1024 pages; anything else takes the general kernel.
-    const bool use_stream = H_kv == 8 && slot_bytes == kStreamRowBytes / 8 && cb_k == cb_v &&
+    const bool use_stream = levels == 16 && H_kv == 8 && slot_bytes == kStreamRowBytes / 8 &&
+                            cb_k == cb_v &&
                             tn <= 16 * kStreamMaxPages && g_allow_stream;
     if (g_split_start && hipEventRecord(g_split_start, st) != hipSuccess)
         return fail(CDA_E_HIP, "cda_decode_full_hmma_v3: hipEventRecord(start) failed");
@@ -1103,10 +1135,15 @@ extern "C" int cda_decode_full_hmma_v3(const void *q, const void *kv_cache, int6
             decode_stream_kernel<4><<<grid, kThreads, 0, st>>>(p);
         else
             decode_stream_kernel<8><<<grid, kThreads, 0, st>>>(p);
+    } else if (levels == 4) {
+        if (group_size == 4)
+            decode_split_kernel<4, 4><<<grid, kThreads, 0, st>>>(p);
+        else
+            decode_split_kernel<8, 4><<<grid, kThreads, 0, st>>>(p);
     } else if (group_size == 4) {
-        decode_split_kernel<4><<<grid, kThreads, 0, st>>>(p);
+        decode_split_kernel<4, 16><<<grid, kThreads, 0, st>>>(p);
     } else {
-        decode_split_kernel<8><<<grid, kThreads, 0, st>>>(p);
+        decode_split_kernel<8, 16><<<grid, kThreads, 0, st>>>(p);
     }
     CDA_LAUNCH_CHECK("decode_split_kernel");
     if (g_split_stop && hipEventRecord(g_split_stop, st) != hipSuccess)

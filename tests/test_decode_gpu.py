@@ -105,6 +105,34 @@ def test_decode_short_sequences(gpu, seed, seq_lens):
         _native.set_stream_kernel(True)
 
 
+K2V2_CASES = [
+    # name, seq_lens, gs, tile_n, fill
+    ("k2v2_ragged", [300, 1, 77, 1031], 4, 0, 0xFF),
+    ("k2v2_gs8", [500, 1200], 8, 0, 0),
+    ("k2v2_tile64", [2000], 4, 64, 0xFF),
+]
+
+
+@pytest.mark.parametrize("name,seq_lens,gs,tile_n,fill", K2V2_CASES, ids=[c[0] for c in K2V2_CASES])
+def test_decode_k2v2_matches_checker(gpu, codebooks, name, seq_lens, gs, tile_n, fill):
+    """2-bit K and V codes (4-level codebook, 80-byte slots; pack_2bit,
+    compression.py:375-397) through the general kernel."""
+    print(f"[decode-k2v2] case={name} seq_lens={seq_lens} gs={gs}", flush=True)
+    cb4 = codebooks["lloyd_beta4"].astype(np.float32)
+    case = make_decode_case(5000 + len(name), seq_lens, H_kv=8, gs=gs, cb=cb4, fill=fill)
+    assert case.cache.shape[-1] == 80
+    out = run_gpu_decode(case, gpu, gs=gs, tile_n=tile_n)
+    check(out, case.expected)
+
+
+def test_decode_k2v2_separate_codebooks(gpu, codebooks):
+    """K2V2 with different K and V codebooks (Lloyd and uniform)."""
+    cbk = codebooks["lloyd_beta4"].astype(np.float32)
+    cbv = codebooks["uniform4"].astype(np.float32)
+    case = make_decode_case(5100, [640, 99], H_kv=8, gs=4, cb=cbk, cb_v=cbv, fill=0xFF)
+    check(run_gpu_decode(case, gpu, gs=4), case.expected)
+
+
 def test_decode_separate_equal_codebooks(gpu):
     """cb_K and cb_V as separate tensors with equal values (the reference
     passes one Compressor's codebook each)."""
