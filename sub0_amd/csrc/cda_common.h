@@ -42,45 +42,21 @@ __device__ __forceinline__ float h2f(uint16_t h) {
     return __half2float(__ushort_as_half(h));
 }
 
-// Correctly rounded (nearest-even) float64 -> float16 bits.  The same integer
-// procedure as cda_oracle_f64_to_f16 in the CPU checker, so both sides agree
-// on every input.
+// float64 -> fp16, round to nearest even, in a few instructions: round to
+// fp32 *to odd* (truncate toward zero, then set the last bit when inexact),
+// then fp32 -> fp16 to nearest even.  fp32 keeps 13 bits more than fp16, so
+// the odd intermediate never creates or hides a tie and the result equals
+// the correctly rounded fp16 of the float64 value (also for fp16 subnormals,
+// overflow to infinity and NaN).
 __device__ __forceinline__ uint16_t f64_to_f16_rn(double v) {
-    uint64_t b = (uint64_t)__double_as_longlong(v);
-    uint32_t sign = (uint32_t)((b >> 48) & 0x8000u);
-    int e = (int)((b >> 52) & 0x7FF);
-    uint64_t m = b & 0xFFFFFFFFFFFFFull;
-    if (e == 0x7FF) return (uint16_t)(sign | 0x7C00u | (m ? 0x200u : 0u));
-    if (e == 0) return (uint16_t)sign;
-    int ue = e - 1023;
-    if (ue > 15) return (uint16_t)(sign | 0x7C00u);
-    uint64_t sig = m | (1ull << 52);
-    int shift;
-    uint32_t hexp;
-    if (ue >= -14) {
-        shift = 42;
-        hexp = (uint32_t)(ue + 15);
-    } else {
-        shift = 42 + (-14 - ue);
-        hexp = 0;
-        if (shift > 63) return (uint16_t)sign;
+    float f = (float)v;                          // nearest even
+    const double back = (double)f;
+    if (back != v && v == v) {
+        uint32_t fb = __float_as_uint(f);
+        if (fabs(back) > fabs(v)) fb -= 1;       // one ulp toward zero
+        f = __uint_as_float(fb | 1u);
     }
-    uint64_t kept = sig >> shift;
-    uint64_t rem = sig & ((1ull << shift) - 1);
-    uint64_t half = 1ull << (shift - 1);
-    if (rem > half || (rem == half && (kept & 1))) kept++;
-    uint32_t out;
-    if (hexp) {
-        if (kept == (1ull << 11)) {
-            kept >>= 1;
-            hexp++;
-        }
-        if (hexp >= 31) return (uint16_t)(sign | 0x7C00u);
-        out = (hexp << 10) | (uint32_t)(kept & 0x3FFu);
-    } else {
-        out = (uint32_t)kept;
-    }
-    return (uint16_t)(sign | out);
+    return __half_as_ushort(__float2half_rn(f));
 }
 
 // Correctly rounded fp32 square root of a float64 value, independent of the

@@ -38,8 +38,55 @@ struct EncodeParams {
     const float *cb_v;
 };
 
-__device__ __forceinline__ double shfl_xor_d(double v, int m) {
-    return __shfl_xor(v, m);
+// Lane l reads lane l ^ M's 32-bit value, without the LDS crossbar: DPP
+// within a row of 16 lanes (M = 1, 2, 4, 8), the row-swap permutes across
+// rows (M = 16, 32).
+template <int M>
+__device__ __forceinline__ uint32_t xor_lane(uint32_t v, int lane) {
+    if constexpr (M == 1) {
+        return __builtin_amdgcn_update_dpp(0u, v, 0xB1, 0xF, 0xF, false);   // quad_perm 1,0,3,2
+    } else if constexpr (M == 2) {
+        return __builtin_amdgcn_update_dpp(0u, v, 0x4E, 0xF, 0xF, false);   // quad_perm 2,3,0,1
+    } else if constexpr (M == 4) {
+        // row_ror:n gives lane l the value of lane (l - n) mod 16 of its row.
+        const uint32_t from_below = __builtin_amdgcn_update_dpp(0u, v, 0x124, 0xF, 0xF, false);
+        const uint32_t from_above = __builtin_amdgcn_update_dpp(0u, v, 0x12C, 0xF, 0xF, false);
+        return (lane & 4) ? from_below : from_above;
+    } else if constexpr (M == 8) {
+        return __builtin_amdgcn_update_dpp(0u, v, 0x128, 0xF, 0xF, false);   // row_ror:8
+    } else if constexpr (M == 16) {
+        const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+        return (lane & 16) ? r[0] : r[1];
+    } else {
+        static_assert(M == 32, "lane distance");
+        const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+        return (lane & 32) ? r[0] : r[1];
+    }
+}
+
+template <int M>
+__device__ __forceinline__ double xor_lane_d(double v, int lane) {
+    const uint64_t b = (uint64_t)__double_as_longlong(v);
+    const uint32_t lo = xor_lane<M>((uint32_t)b, lane);
+    const uint32_t hi = xor_lane<M>((uint32_t)(b >> 32), lane);
+    return __longlong_as_double((long long)(((uint64_t)hi << 32) | lo));
+}
+
+// One butterfly stage across lanes l, l ^ M (element e and e ^ 2M): the lower
+// lane keeps x + partner, the upper one partner - x.  Exact (every partial
+// sum of fp16 values fits float64).
+template <int M>
+__device__ __forceinline__ void bfly_stage(double &x0, double &x1, int lane) {
+    const double p0 = xor_lane_d<M>(x0, lane);
+    const double p1 = xor_lane_d<M>(x1, lane);
+    const double sg = (lane & M) ? -1.0 : 1.0;
+    x0 = fma(sg, x0, p0);
+    x1 = fma(sg, x1, p1);
+}
+
+template <int M>
+__device__ __forceinline__ void tree_stage(double &ss, int lane) {
+    ss = ss + xor_lane_d<M>(ss, lane);
 }
 
 // torch.bucketize(right=False) + neighbour compare (compression.py:298-313):
@@ -66,21 +113,24 @@ __device__ __forceinline__ void encode_vec(uint32_t pair, const float *cb, int l
     // Sylvester butterfly, stage len=1 inside the lane.
     double x0 = a + b, x1 = a - b;
     // Stages len = 2..64: partner element e ^ len lives in lane l ^ (len/2).
-#pragma unroll
-    for (int m = 1; m < 64; m <<= 1) {
-        const double p0 = shfl_xor_d(x0, m);
-        const double p1 = shfl_xor_d(x1, m);
-        const bool low = (lane & m) == 0;
-        x0 = low ? x0 + p0 : p0 - x0;
-        x1 = low ? x1 + p1 : p1 - x1;
-    }
+    bfly_stage<1>(x0, x1, lane);
+    bfly_stage<2>(x0, x1, lane);
+    bfly_stage<4>(x0, x1, lane);
+    bfly_stage<8>(x0, x1, lane);
+    bfly_stage<16>(x0, x1, lane);
+    bfly_stage<32>(x0, x1, lane);
     const double h = (double)__int_as_float(0x3db504f3);   // fp32(1/sqrt(128))
     const uint16_t r0 = f64_to_f16_rn(x0 * h);
     const uint16_t r1 = f64_to_f16_rn(x1 * h);
     const float f0 = h2f(r0), f1 = h2f(r1);
     double ss = (double)f0 * (double)f0 + (double)f1 * (double)f1;
-#pragma unroll
-    for (int m = 1; m < 64; m <<= 1) ss = ss + shfl_xor_d(ss, m);
+    // Pairwise tree in element order: lanes l, l ^ m for m = 1, 2, ..., 32.
+    tree_stage<1>(ss, lane);
+    tree_stage<2>(ss, lane);
+    tree_stage<4>(ss, lane);
+    tree_stage<8>(ss, lane);
+    tree_stage<16>(ss, lane);
+    tree_stage<32>(ss, lane);
     float n = sqrt_f64_to_f32_rn(ss);
     n = (n < 1e-12f) ? 1e-12f : n;     // clamp_min(1e-12); NaN passes through
     nrm = n;
