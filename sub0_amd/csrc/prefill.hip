@@ -57,7 +57,13 @@ constexpr int kKTile = kBN * kKRow;                    // 17408
 constexpr int kTileBytes = kKTile + kD * kVRow;         // + 18432
 constexpr int kLutOff = 2 * kTileBytes;
 constexpr int kLutBytes = 2 * 16 * 64 * 4;             // K and V, 16 codes x 64 columns
-constexpr int kPrefillLds = kLutOff + kLutBytes;
+#ifndef CDA_PF_QLDS
+#define CDA_PF_QLDS 1
+#endif
+// q_rot operands parked in LDS (8 x 16 bytes per lane per wave) instead of
+// registers, when CDA_PF_QLDS is set.
+constexpr int kQOff = kLutOff + kLutBytes;
+constexpr int kPrefillLds = kQOff + (CDA_PF_QLDS ? kWaves * 8 * 64 * 16 : 0);
 
 __device__ __forceinline__ floatx16 mfma32(half8 a, half8 b, floatx16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
@@ -352,14 +358,27 @@ prefill_kernel(PrefillParams p) {
     // 8, so P <= 2^8 and the O rescale is rare after the first tiles);
     // O^T += V^T P^T.  MASK: the tile crosses the causal diagonal or the end
     // of the keys.
+#if CDA_PF_QLDS
+    const uint8_t *qlds = smem + kQOff + (uint32_t)wave * (8 * 64 * 16) + (uint32_t)lane * 16;
+#pragma unroll
+    for (int S = 0; S < 8; ++S)
+        *reinterpret_cast<half8 *>(const_cast<uint8_t *>(qlds) + S * 64 * 16) = qb[S];
+#endif
     auto qk = [&](const uint8_t *buf, int sub) {
         half8 a[8];
 #pragma unroll
         for (int S = 0; S < 8; ++S)
             a[S] = *reinterpret_cast<const half8 *>(buf + k_lane + sub * 32 * kKRow + 32 * S);
+#if CDA_PF_QLDS
+        half8 qv[8];
+#pragma unroll
+        for (int S = 0; S < 8; ++S) qv[S] = *reinterpret_cast<const half8 *>(qlds + S * 64 * 16);
+#else
+        const half8 *qv = qb;
+#endif
         floatx16 acc = {};
 #pragma unroll
-        for (int S = 0; S < 8; ++S) acc = mfma32(a[S], qb[S], acc);
+        for (int S = 0; S < 8; ++S) acc = mfma32(a[S], qv[S], acc);
         return acc;
     };
     // Softmax of one half in place (st <- P); rows = keys kbase + 32*sub +
