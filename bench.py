@@ -8,7 +8,10 @@ A step is one K4V4 split-K decode over the paged cache (Llama-3-8B head
 shape: 32 Q / 8 KV heads, d=128, block 16, randomly permuted block table),
 from unrotated fp16 Q to unrotated fp16 O, with the cache already resident in
 HBM.  The timed region replays a captured hipGraph of the step K times
-between two synchronisations.  Prints ONE JSON line on stdout.
+between two synchronisations, after W untimed warm-up replays that follow a
+0.2-s settle phase of untimed replays (the GPU clocks take ~50 ms to ramp
+from idle; without it the first ~80 steps run ~10 % slow).  Prints ONE JSON
+line on stdout.
 
 * ``value`` = algorithmic HBM bytes per step / time per step (GB/s); the
   bytes are B*N*8*136 (codes + fp32 norms per token and KV head) + Q/O +
@@ -21,7 +24,7 @@ between two synchronisations.  Prints ONE JSON line on stdout.
   V, then one decode step), on the host cores.
 ``--sweep`` also times the 3x3 grid B in {1,4,32} x N in {4K,16K,64K} (median
 of 20 graph replays after 5 warm-ups, as the reference's Table 2) and writes
-it to stderr and gpurun_out/bench_sweep.json.
+it to stderr (and as a JSON list to ``--sweep-out PATH`` when given).
 """
 from __future__ import annotations
 
@@ -144,6 +147,7 @@ def prefill_main(args) -> int:
     res = {}
     for name, dense in (("compressed_tiles", False), ("dense_bridge", True)):
         g = capture(prefill_call(w, dense), args.warmup)
+        settle(g)
         for _ in range(args.warmup):
             g.replay()
         torch.cuda.synchronize()
@@ -245,6 +249,7 @@ def encode_main(args) -> int:
         def call():
             _native.paged_encode(w["k"], w["v"], w["slots"], w["cache"], w["cb"], w["cb"])
         g = capture(call, args.warmup)
+        settle(g)
         for _ in range(args.warmup):
             g.replay()
         torch.cuda.synchronize()
@@ -310,6 +315,17 @@ def decode_call(w, tile_n: int = 0):
                        cb_V=w["cb"], rotation_fp32=w["R"], rotation_fp16=w["R16"],
                        group_size=H_Q // H_KV, block_size=BS, max_seq_len=w["N"])
     return call
+
+
+def settle(g, seconds: float = 0.2):
+    """Untimed replays of ``g`` for ``seconds``: brings the GPU clocks up
+    from idle before the warm-up steps."""
+    import torch
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < seconds:
+        for _ in range(10):
+            g.replay()
+        torch.cuda.synchronize()
 
 
 def capture(fn, warmup: int):
@@ -430,8 +446,9 @@ def load_traffic(kernel, B, N):
 def main(argv=None):
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--sweep-out", default="", help="also write the --sweep rows to this file")
     ap.add_argument("--B", type=int, default=32)
     ap.add_argument("--N", type=int, default=65536)
     ap.add_argument("--sweep", action="store_true")
@@ -480,6 +497,7 @@ def main(argv=None):
     w = make_workload(B, N, dev, identity_bt=args.identity_block_table)
     fn = decode_call(w, args.tile_n)
     g = capture(fn, args.warmup)
+    settle(g)
     for _ in range(args.warmup):
         g.replay()
     torch.cuda.synchronize()
@@ -520,9 +538,8 @@ def main(argv=None):
                 if ww is not w:
                     del ww
                 torch.cuda.empty_cache()
-        out_dir = ROOT / "gpurun_out"
-        if out_dir.is_dir():
-            (out_dir / "bench_sweep.json").write_text(json.dumps(sweep, indent=1) + "\n")
+        if args.sweep_out:
+            Path(args.sweep_out).write_text(json.dumps(sweep, indent=1) + "\n")
 
     cpu = None
     if not args.no_cpu_baseline:

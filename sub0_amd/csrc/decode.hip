@@ -887,28 +887,29 @@ __device__ __forceinline__ float wave_sum(float v) {
 
 // Merge split partials (attention.py:239-272: m* = max m_i, weights
 // exp(m_i - m*), empty splits weigh 0, l clamped at 1e-30), round O_rot to
-// fp16 and unrotate with R^T.  One 256-thread block per (4 q-heads,
-// sequence): wave w merges head w (two dims per lane, 16 splits' loads in
-// flight at a time); R^T is staged in LDS for the epilogue.
+// fp16 and unrotate: out[j] = sum_k fp16(O_rot)[k] * R[j][k].  One 256-thread
+// block per (4 q-heads, sequence): wave w merges head w (two dims per lane, 16
+// splits' loads in flight at a time).  R is staged in LDS in its own row
+// order with rows padded to 132 floats, so the global reads are coalesced,
+// all sixteen per thread are in flight at once, and the epilogue's 16-byte
+// row reads (lane j reads row j) fall in distinct banks.
+constexpr int kRPad = kD + 4;
+
 __global__ void __launch_bounds__(256)
 combine_kernel(const float *part_o, const float *part_ml, const float *R, uint16_t *out,
                int H_q, int n_splits) {
-    __shared__ __align__(16) float RT[kD * kD];
+    __shared__ __align__(16) float Rs[kD * kRPad];
     __shared__ float wts[kHeadsPerBlock][kMaxSplits];
-    __shared__ float orot[kHeadsPerBlock][kD];
+    __shared__ __align__(16) float orot[kHeadsPerBlock][kD];
     const int b = blockIdx.y, t = threadIdx.x;
     const int h0 = blockIdx.x * kHeadsPerBlock;
     const int hh = t >> 6, lane = t & 63;
     const int h = h0 + hh;
-    // R^T into LDS: lane-consecutive j on each write, so the writes do not
-    // conflict; the reads below are row reads of RT.
-    for (int i = t; i < kD * kD / 4; i += 256) {
-        const int j = i % kD, k4 = (i / kD) * 4;
-        const float4 r = *reinterpret_cast<const float4 *>(R + j * kD + k4);
-        RT[(k4 + 0) * kD + j] = r.x;
-        RT[(k4 + 1) * kD + j] = r.y;
-        RT[(k4 + 2) * kD + j] = r.z;
-        RT[(k4 + 3) * kD + j] = r.w;
+    float4 rr[kD * kD / 4 / 256];
+    {
+        const float4 *R4 = reinterpret_cast<const float4 *>(R);
+#pragma unroll
+        for (int u = 0; u < kD * kD / 4 / 256; ++u) rr[u] = R4[t + 256 * u];
     }
     const bool live = h < H_q;
     const int64_t base = (int64_t)b * n_splits * H_q + h;
@@ -928,6 +929,11 @@ combine_kernel(const float *part_o, const float *part_ml, const float *R, uint16
         }
         L = wave_sum(lp);
     }
+#pragma unroll
+    for (int u = 0; u < kD * kD / 4 / 256; ++u) {
+        const int i = t + 256 * u;
+        *reinterpret_cast<float4 *>(Rs + (i >> 5) * kRPad + 4 * (i & 31)) = rr[u];
+    }
     __syncthreads();
     if (live) {
         // Empty splits store zeros, so every partial is read unconditionally.
@@ -946,10 +952,18 @@ combine_kernel(const float *part_o, const float *part_ml, const float *R, uint16
                 o1 = fmaf(wts[hh][s + u], v[u].y, o1);
             }
         }
-        for (; s < n_splits; ++s) {
-            const float2 v = *reinterpret_cast<const float2 *>(po + (int64_t)s * step);
-            o0 = fmaf(wts[hh][s], v.x, o0);
-            o1 = fmaf(wts[hh][s], v.y, o1);
+        if (s < n_splits) {
+            float2 v[16];
+#pragma unroll
+            for (int u = 0; u < 16; ++u)
+                if (s + u < n_splits)
+                    v[u] = *reinterpret_cast<const float2 *>(po + (int64_t)(s + u) * step);
+#pragma unroll
+            for (int u = 0; u < 16; ++u)
+                if (s + u < n_splits) {
+                    o0 = fmaf(wts[hh][s + u], v[u].x, o0);
+                    o1 = fmaf(wts[hh][s + u], v[u].y, o1);
+                }
         }
         const float inv = 1.0f / fmaxf(L, 1e-30f);
         orot[hh][2 * lane] = h2f(__half_as_ushort(__float2half_rn(o0 * inv)));
@@ -957,17 +971,26 @@ combine_kernel(const float *part_o, const float *part_ml, const float *R, uint16
     }
     __syncthreads();
     if (!live) return;
-    const int j = 2 * lane;
+    const float *r0 = Rs + lane * kRPad;
+    const float *r1 = Rs + (lane + 64) * kRPad;
     float a0 = 0.0f, a1 = 0.0f;
 #pragma unroll 8
-    for (int k = 0; k < kD; ++k) {
-        const float2 r = *reinterpret_cast<const float2 *>(RT + k * kD + j);
-        a0 = fmaf(orot[hh][k], r.x, a0);
-        a1 = fmaf(orot[hh][k], r.y, a1);
+    for (int k = 0; k < kD; k += 4) {
+        const float4 o = *reinterpret_cast<const float4 *>(&orot[hh][k]);
+        const float4 x = *reinterpret_cast<const float4 *>(r0 + k);
+        const float4 y = *reinterpret_cast<const float4 *>(r1 + k);
+        a0 = fmaf(o.x, x.x, a0);
+        a0 = fmaf(o.y, x.y, a0);
+        a0 = fmaf(o.z, x.z, a0);
+        a0 = fmaf(o.w, x.w, a0);
+        a1 = fmaf(o.x, y.x, a1);
+        a1 = fmaf(o.y, y.y, a1);
+        a1 = fmaf(o.z, y.z, a1);
+        a1 = fmaf(o.w, y.w, a1);
     }
     const int64_t row = ((int64_t)b * H_q + h) * kD;
-    out[row + j] = __half_as_ushort(__float2half_rn(a0));
-    out[row + j + 1] = __half_as_ushort(__float2half_rn(a1));
+    out[row + lane] = __half_as_ushort(__float2half_rn(a0));
+    out[row + lane + 64] = __half_as_ushort(__float2half_rn(a1));
 }
 
 struct WsLayout {
