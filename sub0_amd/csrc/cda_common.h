@@ -37,6 +37,10 @@ inline size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 
 // ---------------------------------------------------------------- device --
 
+// Forces a lambda (or function) inline: kernels here keep MFMA operands and
+// accumulators in registers, which an out-of-line call would spill.
+#define CDA_INLINE __attribute__((always_inline))
+
 // fp16 bits -> fp32 (exact).
 __device__ __forceinline__ float h2f(uint16_t h) {
     return __half2float(__ushort_as_half(h));

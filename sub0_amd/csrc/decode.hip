@@ -495,7 +495,6 @@ decode_split_kernel(SplitParams p) {
 constexpr int kStreamRowBytes = 8 * 144;
 constexpr int kPageBytes = 16 * kStreamRowBytes;          // one 16-token page, all heads
 constexpr int kHeadPage = 16 * 144;                        // one head's share: 2304 B
-#define CDA_INLINE __attribute__((always_inline))
 
 template <int N>
 using IC = std::integral_constant<int, N>;

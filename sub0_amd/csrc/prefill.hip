@@ -57,13 +57,10 @@ constexpr int kKTile = kBN * kKRow;                    // 17408
 constexpr int kTileBytes = kKTile + kD * kVRow;         // + 18432
 constexpr int kLutOff = 2 * kTileBytes;
 constexpr int kLutBytes = 2 * 16 * 64 * 4;             // K and V, 16 codes x 64 columns
-#ifndef CDA_PF_QLDS
-#define CDA_PF_QLDS 1
-#endif
 // q_rot operands parked in LDS (8 x 16 bytes per lane per wave) instead of
-// registers, when CDA_PF_QLDS is set.
+// registers: the key loop needs the registers more than the LDS bandwidth.
 constexpr int kQOff = kLutOff + kLutBytes;
-constexpr int kPrefillLds = kQOff + (CDA_PF_QLDS ? kWaves * 8 * 64 * 16 : 0);
+constexpr int kPrefillLds = kQOff + kWaves * 8 * 64 * 16;
 
 __device__ __forceinline__ floatx16 mfma32(half8 a, half8 b, floatx16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
@@ -73,6 +70,12 @@ __device__ __forceinline__ uint32_t cvt_pk(float a, float b) {
     typedef float f2 __attribute__((ext_vector_type(2)));
     typedef _Float16 h2 __attribute__((ext_vector_type(2)));
     return __builtin_bit_cast(uint32_t, __builtin_convertvector(f2{a, b}, h2));
+}
+
+// max of three floats (v_maximum3_f32), compiler-visible so that reads of
+// MFMA results before it get their hazard waits.
+__device__ __forceinline__ float max3f(float a, float b, float c) {
+    return __builtin_elementwise_maximum(__builtin_elementwise_maximum(a, b), c);
 }
 
 __device__ __forceinline__ half8 pack8(const floatx16 &c, int base) {
@@ -295,6 +298,9 @@ prefill_kernel(PrefillParams p) {
     const int seq_q = p.cu_q[b + 1] - q_begin;
     const int seq_k = p.seq_k[b];
     // Longest workgroups first: blockIdx.x counts query blocks from the end.
+    // Consecutive workgroups share one (sequence, KV head) and so read the
+    // same keys: ordering the grid by causal work across sequences instead
+    // was measured 30-40 % slower (the L2 working set grows).
     const int q0 = (gridDim.x - 1 - blockIdx.x) * QB;
     if (q0 >= seq_q) return;
     const int off = seq_k - seq_q;                   // bottom-right causal alignment
@@ -350,59 +356,73 @@ prefill_kernel(PrefillParams p) {
     const uint32_t k_lane = (uint32_t)(c32 * kKRow + 16 * u);
     const uint32_t v_lane = (uint32_t)(kKTile + c32 * kVRow + 16 * u);
 
-    // One 64-key tile as two 32-key halves, software-pipelined so that the
-    // softmax (VALU) of one half runs while the MFMAs of the other are in
-    // flight: QK(0), QK(1) | softmax(0) | PV(0) | softmax(1) | PV(1).
-    // S^T = K q_rot^T; online softmax in the log2 domain with a lazy rescale
-    // (the running max moves only when a half's max exceeds it by more than
-    // 8, so P <= 2^8 and the O rescale is rare after the first tiles);
-    // O^T += V^T P^T.  MASK: the tile crosses the causal diagonal or the end
-    // of the keys.
-#if CDA_PF_QLDS
+    // Per 64-key tile: S^T = K q_rot^T; online softmax in the log2 domain with
+    // a lazy rescale (the running max moves only when a tile's max exceeds it
+    // by more than 8, so P <= 2^8 and the O rescale is rare after the first
+    // tiles); O^T += V^T P^T.  MASK: the tile crosses the causal diagonal or
+    // the end of the keys.
+    // |scale| in the exponent; a negative scale flips the sign of q_rot
+    // instead (exact in fp16), so the running max can be taken on raw scores.
+    const float scl = fabsf(p.scale_log2);
+    if (p.scale_log2 < 0.0f) {
+#pragma unroll
+        for (int S = 0; S < 8; ++S) {
+            uint4 w = __builtin_bit_cast(uint4, qb[S]);
+            w.x ^= 0x80008000u; w.y ^= 0x80008000u; w.z ^= 0x80008000u; w.w ^= 0x80008000u;
+            qb[S] = __builtin_bit_cast(half8, w);
+        }
+    }
     const uint8_t *qlds = smem + kQOff + (uint32_t)wave * (8 * 64 * 16) + (uint32_t)lane * 16;
 #pragma unroll
     for (int S = 0; S < 8; ++S)
         *reinterpret_cast<half8 *>(const_cast<uint8_t *>(qlds) + S * 64 * 16) = qb[S];
-#endif
-    auto qk = [&](const uint8_t *buf, int sub) {
-        half8 a[8];
-#pragma unroll
-        for (int S = 0; S < 8; ++S)
-            a[S] = *reinterpret_cast<const half8 *>(buf + k_lane + sub * 32 * kKRow + 32 * S);
-#if CDA_PF_QLDS
-        half8 qv[8];
-#pragma unroll
-        for (int S = 0; S < 8; ++S) qv[S] = *reinterpret_cast<const half8 *>(qlds + S * 64 * 16);
-#else
-        const half8 *qv = qb;
-#endif
-        floatx16 acc = {};
-#pragma unroll
-        for (int S = 0; S < 8; ++S) acc = mfma32(a[S], qv[S], acc);
-        return acc;
-    };
-    // Softmax of one half in place (st <- P); rows = keys kbase + 32*sub +
-    // (r%4) + 4u + 8(r/4), lane = one query.
-    auto softmax = [&](floatx16 &st, int kbase, int sub, auto masked) {
+    // Whole 64-key tile per softmax step: S^T of both 32-key halves (each q
+    // operand read once for both), one running-max update, then O^T += V^T P^T.
+    // The max is taken on raw scores (the scale is positive: a negative scale
+    // was folded into the sign of q_rot) and the scale enters the exponent's
+    // FMA.
+    auto tile = [&](const uint8_t *buf, int kbase, auto masked) {
         constexpr bool MASK = decltype(masked)::value;
+        floatx16 st[2];
+        st[0] = floatx16{};
+        st[1] = floatx16{};
+        // Two k-steps per batch: the operands of the whole tile would not fit.
+#pragma unroll
+        for (int S0 = 0; S0 < 8; S0 += 2) {
+            half8 qv[2], a0[2], a1[2];
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                const int S = S0 + i;
+                qv[i] = *reinterpret_cast<const half8 *>(qlds + S * 64 * 16);
+                a0[i] = *reinterpret_cast<const half8 *>(buf + k_lane + 32 * S);
+                a1[i] = *reinterpret_cast<const half8 *>(buf + k_lane + 32 * kKRow + 32 * S);
+            }
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                st[0] = mfma32(a0[i], qv[i], st[0]);
+                st[1] = mfma32(a1[i], qv[i], st[1]);
+            }
+            asm volatile("" ::: "memory");
+        }
+        if (MASK) {
+#pragma unroll
+            for (int sub = 0; sub < 2; ++sub)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int kpos = kbase + 32 * sub + (r & 3) + 4 * u + 8 * (r >> 2);
+                    if (kpos >= my_kmax) st[sub][r] = -INFINITY;
+                }
+        }
         float mt = -INFINITY;
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            float x = st[r] * p.scale_log2;
-            if (MASK) {
-                const int kpos = kbase + 32 * sub + (r & 3) + 4 * u + 8 * (r >> 2);
-                if (kpos >= my_kmax) x = -INFINITY;
-            }
-            st[r] = x;
-            mt = fmaxf(mt, x);
-        }
+        for (int sub = 0; sub < 2; ++sub)
+#pragma unroll
+            for (int r = 0; r < 16; r += 2) mt = max3f(mt, st[sub][r], st[sub][r + 1]);
         {
             auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mt), __float_as_uint(mt),
                                                        false, false);
-            mt = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
+            mt = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1])) * scl;
         }
-        // Wave-uniform branch (lanes that do not move scale by 1): a per-lane
-        // branch would be if-converted into a select over all of O.
         const bool move = mt > m_run + 8.0f;
         if (__builtin_amdgcn_ballot_w64(move)) {
             const float alpha = move ? __builtin_amdgcn_exp2f(m_run - mt) : 1.0f;  // -inf -> 0
@@ -416,40 +436,28 @@ prefill_kernel(PrefillParams p) {
         const float m_sub = (m_run == -INFINITY) ? 0.0f : m_run;
         float ls = 0.0f;
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const float e = __builtin_amdgcn_exp2f(st[r] - m_sub);
-            st[r] = e;
-            ls += e;
-        }
-        auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(ls), __float_as_uint(ls),
-                                                   false, false);
-        l_run += __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
-    };
-    auto pv = [&](const uint8_t *buf, const floatx16 &pt, int sub) {
-        half8 a[2][4];
+        for (int sub = 0; sub < 2; ++sub)
 #pragma unroll
-        for (int s2 = 0; s2 < 2; ++s2)
+            for (int r = 0; r < 16; ++r) {
+                float e = __builtin_amdgcn_exp2f(fmaf(st[sub][r], scl, -m_sub));
+                if (MASK && st[sub][r] == -INFINITY) e = 0.0f;
+                st[sub][r] = e;
+                ls += e;
+            }
+        {
+            auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(ls), __float_as_uint(ls),
+                                                       false, false);
+            l_run += __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
+        }
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) {
+            half8 a[4];
 #pragma unroll
             for (int T = 0; T < 4; ++T)
-                a[s2][T] = *reinterpret_cast<const half8 *>(
-                    buf + v_lane + T * 32 * kVRow + 32 * (2 * sub + s2));
+                a[T] = *reinterpret_cast<const half8 *>(buf + v_lane + T * 32 * kVRow + 32 * ks);
+            const half8 pb = pack8(st[ks >> 1], 8 * (ks & 1));
 #pragma unroll
-        for (int s2 = 0; s2 < 2; ++s2) {
-            const half8 pb = pack8(pt, 8 * s2);
-#pragma unroll
-            for (int T = 0; T < 4; ++T) o[T] = mfma32(a[s2][T], pb, o[T]);
-        }
-    };
-    auto tile = [&](const uint8_t *buf, int kbase, auto masked) {
-        constexpr bool MASK = decltype(masked)::value;
-        const bool live1 = !MASK || kbase + 32 < wave_kend;
-        floatx16 s0 = qk(buf, 0);
-        softmax(s0, kbase, 0, masked);
-        pv(buf, s0, 0);
-        if (live1) {
-            floatx16 s1 = qk(buf, 1);
-            softmax(s1, kbase, 1, masked);
-            pv(buf, s1, 1);
+            for (int T = 0; T < 4; ++T) o[T] = mfma32(a[T], pb, o[T]);
         }
     };
 
