@@ -159,50 +159,68 @@ struct TileRegs {
     float nv[4];
 };
 
+// Block-table entries of one tile's rows for this thread (paged source): the
+// K row (key tk) and the V rows (keys 4gv..4gv+3, one 16-key block).  They
+// are fetched one tile ahead of the row loads that use them, so no load
+// waits on a block-table load.
+struct TileRows {
+    int32_t bk, bv;
+};
+
+__device__ __forceinline__ int block_of(const PrefillParams &p, int kpos) {
+    return p.bs_shift >= 0 ? (kpos >> p.bs_shift) : (kpos / p.block_size);
+}
+
 template <bool PAGED>
-__device__ __forceinline__ void load_tile(const PrefillParams &p, TileRegs &r, int b, int h,
-                                          int kbase, int nk_valid, int tid) {
-    // K share: key tk = tid >> 3, dims [16c, 16c+16) with c = tid & 7.
-    // V share: keys 4g..4g+3 with g = tid >> 5, dims [4c, 4c+4) with c = tid & 31.
-    // Keys at or past nk_valid are not read (zeros; they are masked later).
+__device__ __forceinline__ TileRows fetch_rows(const PrefillParams &p, const int32_t *bt_row,
+                                               int kbase, int nk_valid, int tid) {
+    TileRows r{0, 0};
+    if (PAGED) {
+        const int tk = tid >> 3, gv = v_gv(tid);
+        if (tk < nk_valid) r.bk = bt_row[block_of(p, kbase + tk)];
+        if (4 * gv < nk_valid) r.bv = bt_row[block_of(p, kbase + 4 * gv)];
+    }
+    return r;
+}
+
+// Source loads of one tile.  K share: key tk = tid >> 3, dims [16c, 16c+16)
+// with c = tid & 7.  V share: keys 4g..4g+3 with g = v_gv(tid), dims
+// [4c, 4c+4) with c = v_cv(tid).  Keys at or past nk_valid are not read
+// (zeros; they are masked later).  Dense rows start at dense_row0 (the
+// sequence's first row of k_rot / v_rot).
+template <bool PAGED>
+__device__ __forceinline__ void load_tile(const PrefillParams &p, TileRegs &r, TileRows rows,
+                                          int64_t dense_row0, int h, int kbase, int nk_valid,
+                                          int tid) {
     const int tk = tid >> 3, ck = tid & 7;
     const int gv = v_gv(tid), cv = v_cv(tid);
     if (PAGED) {
-        const int32_t *bt = p.block_table + (int64_t)b * p.bt_stride;
-        auto row = [&](int kpos) -> const uint8_t * {
-            int blk, in;
-            if (p.bs_shift >= 0) {
-                blk = kpos >> p.bs_shift;
-                in = kpos & (p.block_size - 1);
-            } else {
-                blk = kpos / p.block_size;
-                in = kpos - blk * p.block_size;
-            }
-            const int64_t slot = (int64_t)bt[blk] * p.block_size + in;
-            return p.kv + slot * p.row_bytes + (int64_t)h * p.slot_bytes;
-        };
+        auto in_block = [&](int kpos) { return kpos - block_of(p, kpos) * p.block_size; };
+        const uint8_t *kvh = p.kv + (int64_t)h * p.slot_bytes;
         r.k[0] = r.k[1] = 0u;
         r.nk = 0.0f;
         if (tk < nk_valid) {
-            const uint8_t *rp = row(kbase + tk);
+            const uint8_t *rp =
+                kvh + ((int64_t)rows.bk * p.block_size + in_block(kbase + tk)) * p.row_bytes;
             const uint2 w = *reinterpret_cast<const uint2 *>(rp + 8 * ck);
             r.k[0] = w.x;
             r.k[1] = w.y;
             r.nk = *reinterpret_cast<const float *>(rp + 128);
         }
+        const uint8_t *vp =
+            kvh + ((int64_t)rows.bv * p.block_size + in_block(kbase + 4 * gv)) * p.row_bytes;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const int t = 4 * gv + i;
             r.v[i] = 0u;
             r.nv[i] = 0.0f;
-            if (t < nk_valid) {
-                const uint8_t *rp = row(kbase + t);
+            if (4 * gv + i < nk_valid) {
+                const uint8_t *rp = vp + i * p.row_bytes;
                 r.v[i] = *reinterpret_cast<const uint16_t *>(rp + 64 + 2 * cv);
                 r.nv[i] = *reinterpret_cast<const float *>(rp + 132);
             }
         }
     } else {
-        const int64_t r0 = p.cu_k[b] + kbase;
+        const int64_t r0 = dense_row0 + kbase;
         const int64_t hs = (int64_t)p.H_kv * kD;
         uint4 x0 = make_uint4(0, 0, 0, 0), x1 = x0;
         if (tk < nk_valid) {
@@ -213,12 +231,11 @@ __device__ __forceinline__ void load_tile(const PrefillParams &p, TileRegs &r, i
         }
         r.k[0] = x0.x; r.k[1] = x0.y; r.k[2] = x0.z; r.k[3] = x0.w;
         r.k[4] = x1.x; r.k[5] = x1.y; r.k[6] = x1.z; r.k[7] = x1.w;
+        const uint16_t *vrow = p.v_rot + (r0 + 4 * gv) * hs + h * kD + 4 * cv;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const int t = 4 * gv + i;
             uint2 v = make_uint2(0u, 0u);
-            if (t < nk_valid)
-                v = *reinterpret_cast<const uint2 *>(p.v_rot + (r0 + t) * hs + h * kD + 4 * cv);
+            if (4 * gv + i < nk_valid) v = *reinterpret_cast<const uint2 *>(vrow + i * hs);
             r.v[2 * i] = v.x;
             r.v[2 * i + 1] = v.y;
         }
@@ -462,15 +479,25 @@ prefill_kernel(PrefillParams p) {
     };
 
     const int ntiles = (kend + kBN - 1) / kBN;
+    const int32_t *bt_row = PAGED ? p.block_table + (int64_t)b * p.bt_stride : nullptr;
+    const int64_t dense_row0 = PAGED ? 0 : p.cu_k[b];
     TileRegs cur;
-    if (ntiles > 0) load_tile<PAGED>(p, cur, b, h, 0, min(kBN, kend), tid);
+    TileRows rows_next{0, 0};
+    if (ntiles > 0) {
+        load_tile<PAGED>(p, cur, fetch_rows<PAGED>(p, bt_row, 0, min(kBN, kend), tid),
+                         dense_row0, h, 0, min(kBN, kend), tid);
+        if (ntiles > 1) rows_next = fetch_rows<PAGED>(p, bt_row, kBN, min(kBN, kend - kBN), tid);
+    }
     __syncthreads();   // tables visible
 
     for (int j = 0; j < ntiles; ++j) {
         uint8_t *buf = smem + (j & 1) * kTileBytes;
         store_tile<PAGED>(cur, buf, buf + kKTile, lutk, lutv, tid);
-        if (j + 1 < ntiles)
-            load_tile<PAGED>(p, cur, b, h, (j + 1) * kBN, min(kBN, kend - (j + 1) * kBN), tid);
+        if (j + 1 < ntiles) {
+            const int k1 = (j + 1) * kBN, k2 = (j + 2) * kBN;
+            load_tile<PAGED>(p, cur, rows_next, dense_row0, h, k1, min(kBN, kend - k1), tid);
+            if (j + 2 < ntiles) rows_next = fetch_rows<PAGED>(p, bt_row, k2, min(kBN, kend - k2), tid);
+        }
         __syncthreads();
         const int kbase = j * kBN;
         if (!wave_live || kbase >= wave_kend) continue;
@@ -645,7 +672,8 @@ extern "C" int cda_prefill_paged_hadamard(const void *q, const void *kv_cache, i
                 "cda_prefill_paged_hadamard: H_q / H_kv must be 4 or 8");
     CDA_REQUIRE(levels == 16 && slot_bytes >= 136,
                 "cda_prefill_paged_hadamard: the prefill reads K4V4 caches (16 levels, slot >= 136 B)");
-    CDA_REQUIRE(block_size > 0 && bt_stride > 0, "cda_prefill_paged_hadamard: bad block table");
+    CDA_REQUIRE(block_size > 0 && block_size % 16 == 0 && bt_stride > 0,
+                "cda_prefill_paged_hadamard: block_size must be a positive multiple of 16");
     CDA_REQUIRE(((uintptr_t)q & 15) == 0 && ((uintptr_t)out & 15) == 0 &&
                     ((uintptr_t)kv_cache & 7) == 0 && slot_bytes % 8 == 0,
                 "cda_prefill_paged_hadamard: q/out must be 16-byte and the cache 8-byte aligned");

@@ -72,6 +72,17 @@ def test_prefill_matches_checker(gpu, name, seq_q, seq_k, H_kv, gs, dense):
     check(out, case.expected)
 
 
+@pytest.mark.parametrize("block_size", [32, 48])
+def test_prefill_larger_blocks(gpu, block_size):
+    """Pages of 32 and 48 tokens (the block-table entries are fetched one tile
+    ahead; 48 is not a power of two)."""
+    print(f"[prefill] block_size={block_size}", flush=True)
+    case = make_prefill_case(4400 + block_size, [200, 97], [260, 97], H_kv=8, gs=4,
+                             block_size=block_size, fill=0xFF)
+    out = run_prefill(case, gpu, dense=False)
+    check(out, case.expected)
+
+
 def test_prefill_scale_and_empty_sequence(gpu):
     """Non-default scale; a sequence with no queries between two others."""
     case = make_prefill_case(4100, [33, 0, 70], [33, 50, 100], H_kv=8, gs=4, scale=0.2)
