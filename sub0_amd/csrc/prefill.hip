@@ -42,7 +42,8 @@ constexpr int kWaves = 8;
 constexpr int kThreads = 64 * kWaves;
 constexpr float kLog2e = 1.4426950408889634f;
 
-// LDS: two tile buffers, then the per-code dequant tables (paged source).
+// LDS: two tile buffers, then the code-byte dequant tables (paged source),
+// then the q_rot operands.
 //   K tile   [64 keys][128 dims] fp16, natural dim order, rows padded to 272 B.
 //   V^T tile [128 dims][64 keys] fp16, rows padded to 144 B; within each
 //            16-key group the keys are stored in the MFMA k order (key
@@ -56,7 +57,11 @@ constexpr int kVRow = kBN * 2 + 16;                    // 144
 constexpr int kKTile = kBN * kKRow;                    // 17408
 constexpr int kTileBytes = kKTile + kD * kVRow;         // + 18432
 constexpr int kLutOff = 2 * kTileBytes;
-constexpr int kLutBytes = 2 * 16 * 64 * 4;             // K and V, 16 codes x 64 columns
+// Code-byte tables for K and V: entry x = (cb[x >> 4], cb[x & 15]) in fp32,
+// so one 8-byte read yields both values of a code byte (one copy: 1, 2 and 4
+// interleaved copies measured the same).
+constexpr int kLutEntry = 8;                           // bytes per code byte
+constexpr int kLutBytes = 2 * 256 * kLutEntry;         // 4 KiB
 // q_rot operands parked in LDS (8 x 16 bytes per lane per wave) instead of
 // registers: the key loop needs the registers more than the LDS bandwidth.
 constexpr int kQOff = kLutOff + kLutBytes;
@@ -244,6 +249,13 @@ __device__ __forceinline__ void load_tile(const PrefillParams &p, TileRegs &r, T
 
 // One code byte's two values fp16(cb[code] * norm) from the per-code table
 // (16 rows x 64 lane columns of fp32).
+// One code byte's two values fp16(cb[code] * norm) from the code-byte table
+// (hi nibble first: the even dim).
+__device__ __forceinline__ uint32_t dq_byte(const uint8_t *lut, uint32_t byte, float norm) {
+    const float2 c = *reinterpret_cast<const float2 *>(lut + byte * kLutEntry);
+    return cvt_pk(c.x * norm, c.y * norm);
+}
+
 __device__ __forceinline__ uint32_t dq_pair(const uint8_t *lut, uint32_t byte, uint32_t col,
                                            float norm) {
     const float hi = *reinterpret_cast<const float *>(lut + ((byte >> 4) << 8) + col);
@@ -256,19 +268,18 @@ __device__ __forceinline__ void store_tile(const TileRegs &r, uint8_t *kt, uint8
                                            const uint8_t *lutk, const uint8_t *lutv, int tid) {
     const int tk = tid >> 3, ck = tid & 7;
     const int gv = v_gv(tid), cv = v_cv(tid);
-    const uint32_t col = (uint32_t)(tid & 63) * 4u;
     uint32_t kw[8];      // key tk, dims [16ck, 16ck+16) as fp16 pairs (2j, 2j+1)
     uint32_t pr[4][2];   // key 4gv+i: dims (4cv, 4cv+1), (4cv+2, 4cv+3) as fp16 pairs
     if (PAGED) {
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
             const uint32_t byte = (r.k[j >> 2] >> (8 * (j & 3))) & 0xFFu;
-            kw[j] = dq_pair(lutk, byte, col, r.nk);
+            kw[j] = dq_byte(lutk, byte, r.nk);
         }
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            pr[i][0] = dq_pair(lutv, r.v[i] & 0xFFu, col, r.nv[i]);
-            pr[i][1] = dq_pair(lutv, (r.v[i] >> 8) & 0xFFu, col, r.nv[i]);
+            pr[i][0] = dq_byte(lutv, r.v[i] & 0xFFu, r.nv[i]);
+            pr[i][1] = dq_byte(lutv, (r.v[i] >> 8) & 0xFFu, r.nv[i]);
         }
     } else {
 #pragma unroll
@@ -334,11 +345,14 @@ prefill_kernel(PrefillParams p) {
 
     // ---- tables for the paged source.
     const uint8_t *lutk = smem + kLutOff;
-    const uint8_t *lutv = smem + kLutOff + kLutBytes / 2;
+    const uint8_t *lutv = lutk + kLutBytes / 2;
     if (PAGED) {
-        float *lk = reinterpret_cast<float *>(smem + kLutOff);
-        for (int i = tid; i < 2 * 16 * 64; i += kThreads)
-            lk[i] = (i < 16 * 64) ? p.cb_k[i >> 6] : p.cb_v[(i - 16 * 64) >> 6];
+        float2 *lk = reinterpret_cast<float2 *>(smem + kLutOff);
+        for (int i = tid; i < 2 * 256; i += kThreads) {
+            const int e = i & 255;
+            const float *cb = (i < 256) ? p.cb_k : p.cb_v;
+            lk[i] = make_float2(cb[e >> 4], cb[e & 15]);
+        }
     }
 
     // ---- prologue: q_rot = fp16(q H / sqrt(128)) (compression.py:290-291) as
