@@ -53,42 +53,33 @@ __device__ __forceinline__ float h2f(uint16_t h) {
 // the correctly rounded fp16 of the float64 value (also for fp16 subnormals,
 // overflow to infinity and NaN).
 __device__ __forceinline__ uint16_t f64_to_f16_rn(double v) {
-    float f = (float)v;                          // nearest even
+    const float f = (float)v;                    // nearest even
     const double back = (double)f;
-    if (back != v && v == v) {
-        uint32_t fb = __float_as_uint(f);
-        if (fabs(back) > fabs(v)) fb -= 1;       // one ulp toward zero
-        f = __uint_as_float(fb | 1u);
-    }
-    return __half_as_ushort(__float2half_rn(f));
+    // Branch-free: an exact conversion changes nothing; an inexact one steps
+    // one ulp toward zero if it went past v and sets the sticky last bit.
+    uint32_t fb = __float_as_uint(f) - (fabs(back) > fabs(v) ? 1u : 0u);
+    fb |= (back != v && v == v) ? 1u : 0u;
+    return __half_as_ushort(__float2half_rn(__uint_as_float(fb)));
 }
 
 // Correctly rounded fp32 square root of a float64 value, independent of the
-// hardware sqrt accuracy: start from an approximation and move it until the
+// hardware sqrt accuracy beyond a few float64 ulps: f = fp32(sqrt(x)) is then
+// within one fp32 ulp of the answer, and one branch-free step against the
 // exact fp32 rounding midpoints (25-bit values, whose squares are exact in
-// float64) bracket x.  Same procedure as the CPU checker.
+// float64) moves it there (ties to even).  Same result as the CPU checker's
+// iteration.
 __device__ __forceinline__ float sqrt_f64_to_f32_rn(double x) {
+    const float f = (float)sqrt(x);
+    const int fi = __float_as_int(f);
+    const float up = __int_as_float(fi + 1), dn = __int_as_float(fi - 1);
+    const double mu = ((double)f + (double)up) * 0.5, md = ((double)f + (double)dn) * 0.5;
+    const double mmu = mu * mu, mmd = md * md;
+    const bool odd = (fi & 1) != 0;
+    const bool go_up = mmu < x || (mmu == x && odd);
+    const bool go_dn = mmd > x || (mmd == x && odd);
+    const float r = go_up ? up : (go_dn ? dn : f);
     if (!(x > 0.0)) return (x == 0.0) ? 0.0f : __int_as_float(0x7FC00000);
-    if (x == __longlong_as_double(0x7FF0000000000000ll)) return __int_as_float(0x7F800000);
-    float f = (float)sqrt(x);
-    for (int it = 0; it < 4; ++it) {
-        float up = __int_as_float(__float_as_int(f) + 1);
-        double mid = ((double)f + (double)up) * 0.5;
-        double mm = mid * mid;
-        if (mm < x || (mm == x && (__float_as_int(f) & 1))) {
-            f = up;
-            continue;
-        }
-        float dn = __int_as_float(__float_as_int(f) - 1);
-        double midl = ((double)f + (double)dn) * 0.5;
-        double ml = midl * midl;
-        if (ml > x || (ml == x && (__float_as_int(f) & 1))) {
-            f = dn;
-            continue;
-        }
-        break;
-    }
-    return f;
+    return (x == __longlong_as_double(0x7FF0000000000000ll)) ? __int_as_float(0x7F800000) : r;
 }
 
 }  // namespace cda

@@ -6,21 +6,22 @@
 // (cda/algorithm/compression.py:287-335) and pack_4bit / pack_2bit
 // (:163-179, :375-386).
 //
-// One wave per (token, KV head); it encodes K then V.  Lane l holds
-// elements 2l and 2l+1 of the 128-vector (one coalesced 256-byte read per
-// vector).  The butterfly runs in float64, where every partial sum of fp16
-// inputs is exact, so the rotated value is rounded once, to fp16, exactly as
-// the reference rounds its fp32 matmul result back to the input dtype.  The
-// squared norm is summed in float64 in a fixed lane-tree order and rounded
-// to fp32 with a correctly rounded square root; the division, clamp and the
-// bucketize-style nearest-centroid search run in fp32 as in the reference.
+// A 16-lane row of a wave encodes one 128-vector: lane j holds elements
+// 8j..8j+7 (one 16-byte load), so the first three butterfly stages and the
+// first three levels of the norm tree stay in registers and four stages cross
+// lanes (DPP within the row); a wave encodes four vectors of one role (K or
+// V).  The butterfly runs in float64, where every partial sum of fp16 inputs
+// is exact, so the rotated value is rounded once, to fp16, exactly as the
+// reference rounds its fp32 matmul result back to the input dtype.  The
+// squared norm is summed in float64 in a fixed pairwise-tree order (element
+// order) and rounded to fp32 with a correctly rounded square root; the
+// division, clamp and the bucketize-style nearest-centroid search give the
+// reference's fp32 results.
 #include "cda_common.h"
 
 namespace cda {
 
 namespace {
-
-constexpr int kEncWaves = 4;
 
 struct EncodeParams {
     const uint16_t *k;
@@ -38,146 +39,171 @@ struct EncodeParams {
     const float *cb_v;
 };
 
-// Lane l reads lane l ^ M's 32-bit value, without the LDS crossbar: DPP
-// within a row of 16 lanes (M = 1, 2, 4, 8), the row-swap permutes across
-// rows (M = 16, 32).
+// Lane l reads lane l ^ M's 32-bit value (M = 1, 2, 4, 8) with DPP within its
+// row of 16 lanes, without the LDS crossbar (every source lane exists, so no
+// old value is needed).
 template <int M>
-__device__ __forceinline__ uint32_t xor_lane(uint32_t v, int lane) {
+__device__ __forceinline__ uint32_t xor_lane(uint32_t v) {
     if constexpr (M == 1) {
-        return __builtin_amdgcn_update_dpp(0u, v, 0xB1, 0xF, 0xF, false);   // quad_perm 1,0,3,2
+        return __builtin_amdgcn_mov_dpp(v, 0xB1, 0xF, 0xF, true);   // quad_perm 1,0,3,2
     } else if constexpr (M == 2) {
-        return __builtin_amdgcn_update_dpp(0u, v, 0x4E, 0xF, 0xF, false);   // quad_perm 2,3,0,1
+        return __builtin_amdgcn_mov_dpp(v, 0x4E, 0xF, 0xF, true);   // quad_perm 2,3,0,1
     } else if constexpr (M == 4) {
-        // row_ror:n gives lane l the value of lane (l - n) mod 16 of its row.
-        const uint32_t from_below = __builtin_amdgcn_update_dpp(0u, v, 0x124, 0xF, 0xF, false);
-        const uint32_t from_above = __builtin_amdgcn_update_dpp(0u, v, 0x12C, 0xF, 0xF, false);
-        return (lane & 4) ? from_below : from_above;
-    } else if constexpr (M == 8) {
-        return __builtin_amdgcn_update_dpp(0u, v, 0x128, 0xF, 0xF, false);   // row_ror:8
-    } else if constexpr (M == 16) {
-        const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
-        return (lane & 16) ? r[0] : r[1];
+        // row_half_mirror (lane a of each 8-lane half reads lane 7 - a), then
+        // quad_perm 3,2,1,0 (lane a reads a ^ 3): 7 - (a ^ 3) = a ^ 4.
+        const uint32_t m = __builtin_amdgcn_mov_dpp(v, 0x141, 0xF, 0xF, true);
+        return __builtin_amdgcn_mov_dpp(m, 0x1B, 0xF, 0xF, true);
     } else {
-        static_assert(M == 32, "lane distance");
-        const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
-        return (lane & 32) ? r[0] : r[1];
+        static_assert(M == 8, "lane distance within a row");
+        return __builtin_amdgcn_mov_dpp(v, 0x128, 0xF, 0xF, true);   // row_ror:8
     }
 }
 
 template <int M>
-__device__ __forceinline__ double xor_lane_d(double v, int lane) {
+__device__ __forceinline__ double xor_lane_d(double v) {
     const uint64_t b = (uint64_t)__double_as_longlong(v);
-    const uint32_t lo = xor_lane<M>((uint32_t)b, lane);
-    const uint32_t hi = xor_lane<M>((uint32_t)(b >> 32), lane);
+    const uint32_t lo = xor_lane<M>((uint32_t)b);
+    const uint32_t hi = xor_lane<M>((uint32_t)(b >> 32));
     return __longlong_as_double((long long)(((uint64_t)hi << 32) | lo));
 }
 
-// One butterfly stage across lanes l, l ^ M (element e and e ^ 2M): the lower
-// lane keeps x + partner, the upper one partner - x.  Exact (every partial
-// sum of fp16 values fits float64).
+constexpr int kEncWaves = 4;
+
+// Butterfly stage across lanes j, j ^ M (element bit log2(M) + 3): the lower
+// lane keeps x + partner, the upper one partner - x (exact in float64).
 template <int M>
-__device__ __forceinline__ void bfly_stage(double &x0, double &x1, int lane) {
-    const double p0 = xor_lane_d<M>(x0, lane);
-    const double p1 = xor_lane_d<M>(x1, lane);
+__device__ __forceinline__ void bfly_lanes(double (&x)[8], int lane) {
     const double sg = (lane & M) ? -1.0 : 1.0;
-    x0 = fma(sg, x0, p0);
-    x1 = fma(sg, x1, p1);
-}
-
-template <int M>
-__device__ __forceinline__ void tree_stage(double &ss, int lane) {
-    ss = ss + xor_lane_d<M>(ss, lane);
-}
-
-// torch.bucketize(right=False) + neighbour compare (compression.py:298-313):
-// upper = #{i : !(cb[i] >= x)} (NaN -> L), clamp, ties go to the lower index.
-template <int L>
-__device__ __forceinline__ uint32_t quantize(float x, const float *cb) {
-    int upper = 0;
+    double pt[8];
 #pragma unroll
-    for (int i = 0; i < L; ++i) upper += !(cb[i] >= x);
-    upper = upper > L - 1 ? L - 1 : upper;
-    const int lower = upper - 1 < 0 ? 0 : upper - 1;
-    const float du = fabsf(cb[upper] - x);
-    const float dl = fabsf(x - cb[lower]);
-    return (uint32_t)(du < dl ? upper : lower);
+    for (int i = 0; i < 8; ++i) pt[i] = xor_lane_d<M>(x[i]);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) x[i] = fma(sg, x[i], pt[i]);
 }
 
-// Encode the 128-vector whose elements (2*lane, 2*lane+1) are `pair`; returns
-// the two indices (hi = element 2*lane) and the fp32 norm (same on all lanes).
+// Nearest centroid of x among the sorted L-entry codebook: bucketize-style
+// upper index upper = min(#{i : !(cb[i] >= x)}, L-1) by bisection (the
+// predicate is monotone in i for a sorted codebook; NaN makes it true
+// everywhere, as in the count), then the neighbour compare: the upper index
+// unless the lower neighbour is at least as close (compression.py:298-313).
+// cbl: the codebook in LDS (probes; one shared copy, so lanes reading
+// different entries hit different banks); tri: (cb[2i-1] (cb[0] for i = 0),
+// cb[2i], cb[2i+1]) triples for the last step and the compare.
 template <int L>
-__device__ __forceinline__ void encode_vec(uint32_t pair, const float *cb, int lane,
-                                           uint32_t &i0, uint32_t &i1, float &nrm) {
-    double a = (double)h2f((uint16_t)(pair & 0xFFFFu));
-    double b = (double)h2f((uint16_t)(pair >> 16));
-    // Sylvester butterfly, stage len=1 inside the lane.
-    double x0 = a + b, x1 = a - b;
-    // Stages len = 2..64: partner element e ^ len lives in lane l ^ (len/2).
-    bfly_stage<1>(x0, x1, lane);
-    bfly_stage<2>(x0, x1, lane);
-    bfly_stage<4>(x0, x1, lane);
-    bfly_stage<8>(x0, x1, lane);
-    bfly_stage<16>(x0, x1, lane);
-    bfly_stage<32>(x0, x1, lane);
-    const double h = (double)__int_as_float(0x3db504f3);   // fp32(1/sqrt(128))
-    const uint16_t r0 = f64_to_f16_rn(x0 * h);
-    const uint16_t r1 = f64_to_f16_rn(x1 * h);
-    const float f0 = h2f(r0), f1 = h2f(r1);
-    double ss = (double)f0 * (double)f0 + (double)f1 * (double)f1;
-    // Pairwise tree in element order: lanes l, l ^ m for m = 1, 2, ..., 32.
-    tree_stage<1>(ss, lane);
-    tree_stage<2>(ss, lane);
-    tree_stage<4>(ss, lane);
-    tree_stage<8>(ss, lane);
-    tree_stage<16>(ss, lane);
-    tree_stage<32>(ss, lane);
-    float n = sqrt_f64_to_f32_rn(ss);
-    n = (n < 1e-12f) ? 1e-12f : n;     // clamp_min(1e-12); NaN passes through
-    nrm = n;
-    float u0 = __fdiv_rn(f0, n), u1 = __fdiv_rn(f1, n);
-    u0 = u0 < -1.0f ? -1.0f : (u0 > 1.0f ? 1.0f : u0);
-    u1 = u1 < -1.0f ? -1.0f : (u1 > 1.0f ? 1.0f : u1);
-    i0 = quantize<L>(u0, cb);
-    i1 = quantize<L>(u1, cb);
+__device__ __forceinline__ uint32_t quantize_bisect(float x, const float *cbl, const float4 *tri) {
+    int pos = 0;
+#pragma unroll
+    for (int step = L / 2; step >= 2; step >>= 1)
+        if (!(cbl[pos + step - 1] >= x)) pos += step;
+    const float4 t = tri[pos >> 1];
+    const bool c1 = !(t.y >= x);
+    const int upper = pos + (c1 ? 1 : 0);
+    const float cu = c1 ? t.z : t.y;
+    const float cl = c1 ? t.y : t.x;
+    const int lower = upper - 1 < 0 ? 0 : upper - 1;
+    const float du = fabsf(cu - x);
+    const float dl = fabsf(x - cl);
+    return (uint32_t)(du < dl ? upper : lower);
 }
 
 template <int L>
 __global__ void __launch_bounds__(64 * kEncWaves)
 paged_encode_kernel(EncodeParams p) {
     constexpr int KB = kD * (L == 16 ? 4 : 2) / 8;   // code bytes per role
-    __shared__ float cbs[2][L];
+    __shared__ float4 tri[2][L / 2];
+    __shared__ float cbl[2][L];
+    if (threadIdx.x < L) {
+        const int r = threadIdx.x / (L / 2), i = threadIdx.x % (L / 2);
+        const float *c = r ? p.cb_v : p.cb_k;
+        tri[r][i] = make_float4(c[i ? 2 * i - 1 : 0], c[2 * i], c[2 * i + 1], 0.0f);
+    }
     if (threadIdx.x < 2 * L)
-        cbs[threadIdx.x / L][threadIdx.x % L] =
-            threadIdx.x < L ? p.cb_k[threadIdx.x] : p.cb_v[threadIdx.x - L];
+        cbl[threadIdx.x / L][threadIdx.x % L] =
+            (threadIdx.x < L ? p.cb_k : p.cb_v)[threadIdx.x % L];
     __syncthreads();
 
     const int lane = threadIdx.x & 63;
-    const int64_t item = (int64_t)blockIdx.x * kEncWaves + (threadIdx.x >> 6);
-    if (item >= p.num_tokens * p.H_kv) return;
-    const int64_t t = item / p.H_kv;
-    const int h = (int)(item % p.H_kv);
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int role = wave >> 1;                       // waves 0,1: K; 2,3: V (wave-uniform)
+    const int j = lane & 15;
+    const int64_t items = p.num_tokens * p.H_kv;
+    const int64_t item = (int64_t)blockIdx.x * 8 + 4 * (wave & 1) + (lane >> 4);
+    const bool valid = item < items;
+    const int64_t t = valid ? item / p.H_kv : 0;
+    const int h = valid ? (int)(item - t * p.H_kv) : 0;
+
+    double x[8];
+    {
+        const uint16_t *src = role == 0 ? p.k + t * p.k_stride + (int64_t)h * kD
+                                        : p.v + t * p.v_stride + (int64_t)h * kD;
+        uint4 w = make_uint4(0, 0, 0, 0);
+        if (valid) w = reinterpret_cast<const uint4 *>(src)[j];
+        const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            x[2 * i] = (double)h2f((uint16_t)(ws[i] & 0xFFFFu));
+            x[2 * i + 1] = (double)h2f((uint16_t)(ws[i] >> 16));
+        }
+    }
+    // Sylvester butterflies: element bits 0-2 in registers, bits 3-6 across
+    // lanes j ^ 1, 2, 4, 8 (exact in float64).
+#pragma unroll
+    for (int m = 1; m < 8; m <<= 1)
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+            if (!(i & m)) {
+                const double a = x[i], b = x[i | m];
+                x[i] = a + b;
+                x[i | m] = a - b;
+            }
+    bfly_lanes<1>(x, lane);
+    bfly_lanes<2>(x, lane);
+    bfly_lanes<4>(x, lane);
+    bfly_lanes<8>(x, lane);
+    const double hsc = (double)__int_as_float(0x3db504f3);   // fp32(1/sqrt(128))
+    float f[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) f[i] = h2f(f64_to_f16_rn(x[i] * hsc));
+    // Squared norm: the pairwise tree in element order.
+    double sq[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) sq[i] = (double)f[i] * (double)f[i];
+    double ss = ((sq[0] + sq[1]) + (sq[2] + sq[3])) + ((sq[4] + sq[5]) + (sq[6] + sq[7]));
+    ss = ss + xor_lane_d<1>(ss);
+    ss = ss + xor_lane_d<2>(ss);
+    ss = ss + xor_lane_d<4>(ss);
+    ss = ss + xor_lane_d<8>(ss);
+    float n = sqrt_f64_to_f32_rn(ss);
+    n = (n < 1e-12f) ? 1e-12f : n;     // clamp_min(1e-12); NaN passes through
+    // u = RN32(f / n) as RN32(f * RN64(1 / n)): the float64 product is within
+    // 2^-52 (relative) of f / n, and a quotient of two 24-bit numbers is never
+    // a 25-bit rounding midpoint and, when not one, lies at least 2^-49 from
+    // every midpoint, so the final rounding equals the correctly rounded
+    // quotient (NaN, infinity and zero propagate as in the division).
+    const double rn = 1.0 / (double)n;
+    uint32_t idx[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        float u = (float)((double)f[i] * rn);
+        u = u < -1.0f ? -1.0f : (u > 1.0f ? 1.0f : u);
+        idx[i] = quantize_bisect<L>(u, cbl[role], tri[role]);
+    }
+    if (!valid) return;
     const int64_t slot = p.slot_mapping[t];
     if (slot < 0 || slot >= p.num_slots) return;
     uint8_t *dst = p.cache + slot * p.row_bytes + (int64_t)h * p.slot_bytes;
-
+    uint8_t *codes = dst + role * KB;
+    if (L == 16) {
+        uint32_t wv = 0;
 #pragma unroll
-    for (int role = 0; role < 2; ++role) {
-        const uint16_t *src = role == 0 ? p.k + t * p.k_stride + (int64_t)h * kD
-                                        : p.v + t * p.v_stride + (int64_t)h * kD;
-        const uint32_t pair = reinterpret_cast<const uint32_t *>(src)[lane];
-        uint32_t i0, i1;
-        float nrm;
-        encode_vec<L>(pair, cbs[role], lane, i0, i1, nrm);
-        uint8_t *codes = dst + role * KB;
-        if (L == 16) {
-            codes[lane] = (uint8_t)((i0 << 4) | i1);
-        } else {
-            const uint32_t nib = (i0 << 2) | i1;          // dims 2l, 2l+1
-            const uint32_t other = (uint32_t)__shfl_xor((int)nib, 1);
-            if ((lane & 1) == 0) codes[lane >> 1] = (uint8_t)((nib << 4) | other);
-        }
-        if (lane == 0) *reinterpret_cast<float *>(dst + 2 * KB + 4 * role) = nrm;
+        for (int b = 0; b < 4; ++b) wv |= ((idx[2 * b] << 4) | idx[2 * b + 1]) << (8 * b);
+        *reinterpret_cast<uint32_t *>(codes + 4 * j) = wv;
+    } else {
+        const uint32_t b0 = (idx[0] << 6) | (idx[1] << 4) | (idx[2] << 2) | idx[3];
+        const uint32_t b1 = (idx[4] << 6) | (idx[5] << 4) | (idx[6] << 2) | idx[7];
+        *reinterpret_cast<uint16_t *>(codes + 2 * j) = (uint16_t)(b0 | (b1 << 8));
     }
+    if (j == 0) *reinterpret_cast<float *>(dst + 2 * KB + 4 * role) = n;
 }
 
 }  // namespace
@@ -219,9 +245,9 @@ extern "C" int cda_paged_encode_fused(const void *k, const void *v, int64_t k_st
     p.cb_k = cb_k;
     p.cb_v = cb_v;
     const int64_t items = num_tokens * H_kv;
-    const int64_t blocks = (items + kEncWaves - 1) / kEncWaves;
-    CDA_REQUIRE(blocks < ((int64_t)1 << 31), "cda_paged_encode_fused: too many tokens");
     hipStream_t st = static_cast<hipStream_t>(stream);
+    const int64_t blocks = (items + 7) / 8;
+    CDA_REQUIRE(blocks < ((int64_t)1 << 31), "cda_paged_encode_fused: too many tokens");
     if (levels == 16)
         paged_encode_kernel<16><<<dim3((unsigned)blocks), 64 * kEncWaves, 0, st>>>(p);
     else

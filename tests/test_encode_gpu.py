@@ -9,10 +9,10 @@ from oracle import synth
 pytestmark = pytest.mark.gpu
 
 
-def expected_cache(k, v, slots, cb, num_slots, slot_bytes, sentinel):
+def expected_cache(k, v, slots, cb, num_slots, slot_bytes, sentinel, cb_v=None):
     T, H_kv, _ = k.shape
     kp, kn, _ = O.encode(k, cb)
-    vp, vn, _ = O.encode(v, cb)
+    vp, vn, _ = O.encode(v, cb if cb_v is None else cb_v)
     kb = kp.shape[-1]
     cache = np.full((num_slots, H_kv, slot_bytes), sentinel, dtype=np.uint8)
     for t in range(T):
@@ -26,13 +26,14 @@ def expected_cache(k, v, slots, cb, num_slots, slot_bytes, sentinel):
     return cache
 
 
-def run_gpu_encode(dev, k, v, slots, cb, num_slots, slot_bytes, sentinel):
+def run_gpu_encode(dev, k, v, slots, cb, num_slots, slot_bytes, sentinel, cb_v=None):
     from sub0_amd import _native
     cache = torch.full((num_slots, k.shape[1], slot_bytes), sentinel, dtype=torch.uint8,
                        device=dev)
     cbt = torch.from_numpy(cb).to(dev)
+    cbv = cbt if cb_v is None else torch.from_numpy(cb_v).to(dev)
     _native.paged_encode(torch.from_numpy(k).to(dev), torch.from_numpy(v).to(dev),
-                         torch.from_numpy(slots.astype(np.int32)).to(dev), cache, cbt, cbt)
+                         torch.from_numpy(slots.astype(np.int32)).to(dev), cache, cbt, cbv)
     torch.cuda.synchronize()
     return cache.cpu().numpy()
 
@@ -49,6 +50,24 @@ def test_encode_bit_exact(gpu, codebooks, levels, slot_bytes):
     slots[::17] = -1                      # padding tokens are skipped
     exp = expected_cache(k, v, slots, cb, num_slots, slot_bytes, 0xA5)
     got = run_gpu_encode(gpu, k, v, slots, cb, num_slots, slot_bytes, 0xA5)
+    bad = np.argwhere(got != exp)
+    assert bad.size == 0, f"{len(bad)} mismatching bytes, first {bad[:5].tolist()}"
+
+
+@pytest.mark.parametrize("levels,H_kv", [(16, 8), (4, 8), (16, 3)])
+def test_encode_separate_codebooks(gpu, codebooks, levels, H_kv):
+    """K and V with different codebooks (each role reads its own), and a head
+    count that leaves a partial group of vectors in the last wave."""
+    print(f"[encode] separate codebooks levels={levels} H_kv={H_kv}", flush=True)
+    cb_k = codebooks["lloyd_beta16" if levels == 16 else "lloyd_beta4"]
+    cb_v = codebooks["uniform16" if levels == 16 else "uniform4"]
+    T = 77
+    k = synth.kv_with_outliers(511, (T, H_kv, 128))
+    v = synth.normal_f16(512, (T, H_kv, 128))
+    slots = np.arange(T, dtype=np.int64)[::-1].copy()
+    sb = 144 if levels == 16 else 80
+    exp = expected_cache(k, v, slots, cb_k, T, sb, 0x3C, cb_v=cb_v)
+    got = run_gpu_encode(gpu, k, v, slots, cb_k, T, sb, 0x3C, cb_v=cb_v)
     bad = np.argwhere(got != exp)
     assert bad.size == 0, f"{len(bad)} mismatching bytes, first {bad[:5].tolist()}"
 
