@@ -179,7 +179,8 @@ void cda_oracle_quantize(const float *x, int64_t n, const float *cb, int L, uint
 /* Correctly rounded fp32 square root of a float64 value: move an
    approximation until the exact fp32 rounding midpoints (25-bit values whose
    squares are exact in float64) bracket x; ties go to even.  The HIP encoder
-   uses the same procedure. */
+   takes the same midpoint test as one branch-free step from fp32(sqrt(x)),
+   which is within one fp32 ulp of the answer. */
 static float sqrt_f64_to_f32_rn(double x) {
     if (!(x > 0.0)) return x == 0.0 ? 0.0f : NAN;
     if (isinf(x)) return INFINITY;
