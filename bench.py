@@ -297,6 +297,229 @@ def encode_main(args) -> int:
     return 0
 
 
+# ------------------------------------------------------------------ e2e ---
+# BASELINE config 4 without vLLM (not installed here or on the GPU box): a
+# random-init Mistral-7B-shaped decoder driven through the cda_v2 backend's
+# Impl exactly as vLLM's attention layer calls it (do_kv_cache_update, then
+# forward with CDAv2AttentionMetadata over a vLLM-shaped (nb, 16, 8, 72) fp16
+# cache per layer).  The GEMMs, norms, RoPE and sampling are plain PyTorch.
+
+class E2EModel:
+    """Mistral-shaped decoder: pre-RMSNorm, fused QKV, RoPE (theta 1e6),
+    SwiGLU, greedy LM head; fp16 weights ~ N(0, 0.02^2) from a seeded GPU
+    generator."""
+
+    def __init__(self, dev, *, layers=32, heads=32, kv_heads=8, ffn=14336, vocab=32000,
+                 seed=0xCDA4):
+        import torch
+        self.dev, self.L, self.H, self.Hkv, self.D = dev, layers, heads, kv_heads, D
+        self.hidden = heads * D
+        g = torch.Generator(device=dev).manual_seed(seed)
+
+        def w(*shape):
+            return torch.randn(*shape, generator=g, device=dev, dtype=torch.float16) * 0.02
+        hd = self.hidden
+        self.emb = w(vocab, hd)
+        self.lm = w(vocab, hd)
+        self.layers = [dict(qkv=w(hd + 2 * kv_heads * D, hd), o=w(hd, hd), gu=w(2 * ffn, hd),
+                            down=w(hd, ffn)) for _ in range(layers)]
+        self.inv_freq = 1.0 / (1e6 ** (torch.arange(0, D, 2, device=dev, dtype=torch.float32) / D))
+        from sub0_amd.cda.kernels_cuda.vllm_integration import cda_attn_v2 as A
+        self.A = A
+        self.impl = A.get_backend_classes()[1](heads, D, 1.0 / D ** 0.5, num_kv_heads=kv_heads)
+
+    @staticmethod
+    def rmsnorm(x):
+        import torch
+        return torch.nn.functional.rms_norm(x.float(), (x.shape[-1],), eps=1e-5).to(x.dtype)
+
+    def rope_tables(self, pos):
+        import torch
+        f = pos.float()[:, None] * self.inv_freq[None]
+        return torch.cos(f)[:, None, :], torch.sin(f)[:, None, :]
+
+    @staticmethod
+    def rope(x, cs):
+        import torch
+        c, s = cs
+        x1, x2 = x[..., :D // 2].float(), x[..., D // 2:].float()
+        return torch.cat([x1 * c - x2 * s, x2 * c + x1 * s], -1).to(x.dtype)
+
+    def attention(self, q, k, v, caches, md):
+        """The backend calls of every layer alone (cache update + attention) on
+        fixed q, k, v: what the attention share of a step is measured on."""
+        import torch
+        a = torch.empty(q.shape[0], self.hidden, dtype=torch.float16, device=self.dev)
+        for li in range(self.L):
+            self.impl.do_kv_cache_update(None, k, v, caches[li], md.slot_mapping)
+            self.impl.forward(None, q, k, v, caches[li], md, a)
+        return a
+
+    def forward(self, tok, pos, caches, md):
+        """One pass over T tokens; returns the logits of every row."""
+        import torch
+        T = tok.shape[0]
+        x = self.emb[tok]
+        cs = self.rope_tables(pos)
+        for li, p in enumerate(self.layers):
+            h = self.rmsnorm(x)
+            qkv = h @ p["qkv"].t()
+            q = qkv[:, :self.hidden].view(T, self.H, D)
+            k = qkv[:, self.hidden:self.hidden + self.Hkv * D].view(T, self.Hkv, D)
+            v = qkv[:, self.hidden + self.Hkv * D:].view(T, self.Hkv, D).contiguous()
+            q, k = self.rope(q, cs), self.rope(k, cs)
+            self.impl.do_kv_cache_update(None, k, v, caches[li], md.slot_mapping)
+            a = torch.empty(T, self.hidden, dtype=torch.float16, device=self.dev)
+            self.impl.forward(None, q, k, v, caches[li], md, a)
+            x = x + a @ p["o"].t()
+            gu = self.rmsnorm(x) @ p["gu"].t()
+            g, u = gu.chunk(2, -1)
+            x = x + (torch.nn.functional.silu(g) * u) @ p["down"].t()
+        return self.rmsnorm(x) @ self.lm.t()
+
+
+def e2e_run(dev, *, B=32, prefix=16384, steps=256, layers=32, heads=32, kv_heads=8,
+            ffn=14336, vocab=32000, seed=0xCDA4, check_eager=0):
+    """Prefill B random prefixes through the model (one request per forward),
+    then `steps` greedy decode steps of all B requests as replays of one
+    captured step (state advanced inside the graph).  Returns a dict of
+    timings; with check_eager > 0 also the tokens of that many eager steps
+    run from the same state, for comparison with the replays."""
+    import torch
+    m = E2EModel(dev, layers=layers, heads=heads, kv_heads=kv_heads, ffn=ffn, vocab=vocab,
+                 seed=seed)
+    A = m.A
+    cap = prefix + steps + 1
+    nbs = (cap + BS - 1) // BS
+    gen = torch.Generator().manual_seed(seed)
+    perm = torch.randperm(B * nbs, generator=gen).to(torch.int32)
+    bt = perm.view(B, nbs).to(dev)
+    caches = [torch.zeros(B * nbs, BS, kv_heads, 72, dtype=torch.float16, device=dev)
+              for _ in range(layers)]
+    prompts = torch.randint(0, vocab, (B, prefix), generator=gen).to(dev)
+
+    def slots_of(b_idx, pos):
+        return (bt[b_idx, pos // BS].to(torch.int64) * BS + pos % BS)
+
+    # -- prefill, one request per pass (vLLM would chunk; the kernels are the same)
+    first = torch.empty(B, dtype=torch.int64, device=dev)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    ar = torch.arange(prefix, device=dev, dtype=torch.int64)
+    for b in range(B):
+        md = A.CDAv2AttentionMetadata(
+            num_actual_tokens=prefix, num_reqs=1, max_query_len=prefix, max_seq_len=prefix,
+            query_start_loc=torch.tensor([0, prefix], dtype=torch.int32, device=dev),
+            seq_lens=torch.tensor([prefix], dtype=torch.int32, device=dev),
+            block_table=bt[b:b + 1], slot_mapping=slots_of(b, ar))
+        logits = m.forward(prompts[b], ar, caches, md)
+        first[b] = logits[-1].argmax()
+        if b % 8 == 7:
+            log(f"e2e: prefilled {b + 1}/{B} requests")
+    torch.cuda.synchronize()
+    prefill_s = time.perf_counter() - t0
+
+    # -- decode state (static buffers the captured step reads and advances)
+    rows = torch.arange(B, device=dev)
+    tok = first.clone()
+    pos = torch.full((B,), prefix, dtype=torch.int64, device=dev)
+    seq = torch.full((B,), prefix + 1, dtype=torch.int32, device=dev)
+    slots = slots_of(rows, pos)
+    md = A.CDAv2AttentionMetadata(
+        num_actual_tokens=B, num_reqs=B, max_query_len=1, max_seq_len=cap,
+        query_start_loc=torch.arange(B + 1, dtype=torch.int32, device=dev),
+        seq_lens=seq, block_table=bt, slot_mapping=slots)
+
+    def step():
+        logits = m.forward(tok, pos, caches, md)
+        tok.copy_(logits.argmax(-1))
+        pos.add_(1)
+        seq.add_(1)
+        slots.copy_(slots_of(rows, pos))
+
+    produced = [first.clone()]
+    step()                                  # step 1 eagerly (warm-up, allocator)
+    produced.append(tok.clone())
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g):
+            step()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    eager_tokens = None
+    if check_eager:
+        # Replays vs eager steps from the same state: snapshot, run eagerly, restore.
+        snap = [x.clone() for x in (tok, pos, seq, slots)] + [c.clone() for c in caches]
+        eager_tokens = []
+        for _ in range(check_eager):
+            step()
+            eager_tokens.append(tok.clone())
+        for dst, src in zip([tok, pos, seq, slots] + caches, snap):
+            dst.copy_(src)
+        del snap
+        torch.cuda.synchronize()
+    n = steps - 1
+    t0 = time.perf_counter()
+    for i in range(n):
+        g.replay()
+        if i < check_eager:
+            produced.append(tok.clone())
+    torch.cuda.synchronize()
+    decode_s = time.perf_counter() - t0
+    if not check_eager:
+        produced.append(tok.clone())
+
+    # -- attention share: every layer's cache update + attention alone (same
+    # metadata; it rewrites the next token's slots, which the next step
+    # overwrites before reading)
+    qa = torch.randn(B, heads, D, generator=torch.Generator(device=dev).manual_seed(1),
+                     device=dev, dtype=torch.float16)
+    ka = qa[:, :kv_heads].contiguous()
+    va = qa[:, kv_heads:2 * kv_heads].contiguous()
+    ga = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        m.attention(qa, ka, va, caches, md)          # warm-up outside the graph
+        torch.cuda.current_stream().synchronize()
+        with torch.cuda.graph(ga):
+            m.attention(qa, ka, va, caches, md)
+    torch.cuda.synchronize()
+    reps = max(1, min(n, 50))
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        ga.replay()
+    torch.cuda.synchronize()
+    attn_s = (time.perf_counter() - t0) / reps
+    return dict(prefill_s=prefill_s, decode_s=decode_s, decode_steps=n,
+                step_ms=decode_s / n * 1e3, attn_ms=attn_s * 1e3,
+                tokens_per_s=B * n / decode_s, produced=produced, eager_tokens=eager_tokens)
+
+
+def e2e_main(args) -> int:
+    """--e2e: BASELINE config 4 (not the headline metric); one JSON line."""
+    import torch
+    dev = torch.device("cuda:0")
+    r = e2e_run(dev, B=args.e2e_batch, prefix=args.e2e_prefix, steps=args.e2e_steps)
+    out = {"metric": "end-to-end decode tokens/s through the cda_v2 backend (BASELINE config 4)",
+           "value": round(r["tokens_per_s"], 1), "unit": "tokens/s", "n_gpus": 1,
+           "steps": r["decode_steps"], "ms_per_step": round(r["step_ms"], 3),
+           "higher_is_better": True, "dtype": "fp16 weights/activations, K4V4 cache",
+           "data": "synthetic (random-init weights, random prompt tokens)",
+           "config": {"workload": f"random-init Mistral-7B-shaped decoder (32 layers, hidden 4096, "
+                                  f"32 Q / 8 KV heads, d=128, SwiGLU 14336, RMSNorm, RoPE), "
+                                  f"{args.e2e_batch} sequences x {args.e2e_prefix}-token prefix, "
+                                  f"{args.e2e_steps} greedy decode steps (first from the prefill, "
+                                  f"one eager, the rest graph replays)",
+                      "driver": "cda_v2 backend Impl with stand-in vLLM metadata (vLLM absent)"},
+           "attention_ms_per_step": round(r["attn_ms"], 3),
+           "attention_share": round(r["attn_ms"] / r["step_ms"], 3),
+           "prefill_s": round(r["prefill_s"], 2)}
+    print(json.dumps(out), flush=True)
+    return 0
+
+
 def decode_call(w, tile_n: int = 0):
     from sub0_amd.cda.kernels_cuda.wrappers import decode_hmma_v1
 
@@ -459,6 +682,12 @@ def main(argv=None):
                     help="BASELINE config 2: fused paged encode, K4V4 and K2V2 (one JSON line)")
     ap.add_argument("--prefill", action="store_true",
                     help="time BASELINE config 3 (varlen causal prefill) instead of decode")
+    ap.add_argument("--e2e", action="store_true",
+                    help="BASELINE config 4: decode loop of a Mistral-shaped model through the "
+                         "cda_v2 backend (one JSON line)")
+    ap.add_argument("--e2e-batch", type=int, default=32)
+    ap.add_argument("--e2e-prefix", type=int, default=16384)
+    ap.add_argument("--e2e-steps", type=int, default=256)
     ap.add_argument("--general-kernel", action="store_true",
                     help="forbid the page-streaming split kernel (A/B diagnostic)")
     ap.add_argument("--identity-block-table", action="store_true",
@@ -490,6 +719,8 @@ def main(argv=None):
         return prefill_main(args)
     if args.encode:
         return encode_main(args)
+    if args.e2e:
+        return e2e_main(args)
     if args.general_kernel:
         _native.set_stream_kernel(False)
     B, N = args.B, args.N
