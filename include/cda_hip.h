@@ -102,7 +102,8 @@ int cda_decode_set_stream_kernel(int enable);
  * cb_k, cb_v:    (levels,) fp32, levels = 16 (K4V4) or 4 (K2V2).
  * Per (token, head, role): Hadamard-128 (exact float64 butterfly, one fp16
  * rounding), fp32 L2 norm clamped to 1e-12, nearest centroid with ties to
- * the lower index, MSB-first packing (compression.py:315-335).
+ * the lower index (codebooks sorted ascending, as bucketize requires),
+ * MSB-first packing (compression.py:315-335).
  */
 int cda_paged_encode_fused(const void *k, const void *v, int64_t k_stride, int64_t v_stride,
                            const int32_t *slot_mapping, int64_t num_tokens, void *flat_cache,
@@ -123,6 +124,7 @@ int cda_paged_encode_fused(const void *k, const void *v, int64_t k_stride, int64
  *   q, out:        (T, H_q, 128) fp16, unrotated; T = cu_seqlens_q[B].
  *   cu_seqlens_q:  (B+1,) int32.   seq_lens: (B,) int32 key lengths.
  *   H_q / H_kv:    4 or 8.         levels: 16.
+ *   block_size:    a multiple of 16 (pages of 16 tokens or more).
  */
 int cda_prefill_paged_hadamard(const void *q, const void *kv_cache, int64_t num_slots,
                                int slot_bytes, int H_kv, const int32_t *block_table,
