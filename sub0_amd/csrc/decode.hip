@@ -597,10 +597,16 @@ decode_stream_kernel(SplitParams p) {
         for (int s = 0; s < 4; ++s) qb[s] = *reinterpret_cast<const uint4 *>(qg + 8 * s);
     }
     {
+        // The codebook goes through LDS first: a global load per table entry
+        // would put 32 dependent memory round trips in every thread's
+        // prologue.
+        __shared__ float cbs[16];
+        if (tid < 16) cbs[tid] = p.cb_k[tid];
+        __syncthreads();
         uint32_t *lut = reinterpret_cast<uint32_t *>(smem);
         for (int i = tid; i < kLut2Bytes / 4; i += kThreads) {
             const int e = i >> 6;
-            lut[i] = __float_as_uint(p.cb_k[(i & 1) ? (e & 15) : (e >> 4)]);
+            lut[i] = __float_as_uint(cbs[(i & 1) ? (e & 15) : (e >> 4)]);
         }
     }
     __syncthreads();
