@@ -507,10 +507,14 @@ typedef unsigned v4u32 __attribute__((ext_vector_type(4)));
 // One 16-byte-per-lane direct-to-LDS load: lane l's 16 bytes at rsrc+voff go
 // to LDS address lds_base + 16*l.  Issued through asm so the compiler does not
 // track these asynchronous LDS writes (its tracking is conservative and would
-// serialise the ring); completion is ordered by the explicit vmcnt waits.
+// serialise the ring); completion is ordered by the explicit vmcnt waits.  M0
+// (the LDS base operand) is saved and restored around the load, so the
+// compiler's own use of M0 is never disturbed.
 __device__ __forceinline__ void dma_page_chunk(v4u32 rsrc, uint32_t voff, uint32_t lds_base) {
-    asm volatile("s_mov_b32 m0, %2\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds"
-                 :: "v"(voff), "s"(rsrc), "s"(lds_base) : "memory", "m0");
+    uint32_t saved;
+    asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %3\n\t"
+                 "buffer_load_dwordx4 %1, %2, 0 offen lds\n\ts_mov_b32 m0, %0"
+                 : "=&s"(saved) : "v"(voff), "s"(rsrc), "s"(lds_base) : "memory");
 }
 
 __device__ __forceinline__ uint32_t lds_u32addr(const void *p) {
