@@ -126,11 +126,13 @@ paged_encode_kernel(EncodeParams p) {
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int role = wave >> 1;                       // waves 0,1: K; 2,3: V (wave-uniform)
     const int j = lane & 15;
-    const int64_t items = p.num_tokens * p.H_kv;
-    const int64_t item = (int64_t)blockIdx.x * 8 + 4 * (wave & 1) + (lane >> 4);
+    // (token, head) item of this row; fewer than 2^31 items (checked on the host).
+    const uint32_t items = (uint32_t)(p.num_tokens * p.H_kv);
+    const uint32_t item = blockIdx.x * 8u + 4u * (uint32_t)(wave & 1) + (uint32_t)(lane >> 4);
     const bool valid = item < items;
-    const int64_t t = valid ? item / p.H_kv : 0;
-    const int h = valid ? (int)(item - t * p.H_kv) : 0;
+    const uint32_t t32 = valid ? item / (uint32_t)p.H_kv : 0u;
+    const int h = valid ? (int)(item - t32 * (uint32_t)p.H_kv) : 0;
+    const int64_t t = t32;
 
     double x[8];
     {
@@ -245,9 +247,9 @@ extern "C" int cda_paged_encode_fused(const void *k, const void *v, int64_t k_st
     p.cb_k = cb_k;
     p.cb_v = cb_v;
     const int64_t items = num_tokens * H_kv;
+    CDA_REQUIRE(items < ((int64_t)1 << 31), "cda_paged_encode_fused: too many tokens x heads");
     hipStream_t st = static_cast<hipStream_t>(stream);
     const int64_t blocks = (items + 7) / 8;
-    CDA_REQUIRE(blocks < ((int64_t)1 << 31), "cda_paged_encode_fused: too many tokens");
     if (levels == 16)
         paged_encode_kernel<16><<<dim3((unsigned)blocks), 64 * kEncWaves, 0, st>>>(p);
     else
