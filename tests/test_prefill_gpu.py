@@ -72,6 +72,15 @@ def test_prefill_matches_checker(gpu, name, seq_q, seq_k, H_kv, gs, dense):
     check(out, case.expected)
 
 
+@pytest.mark.parametrize("dense", [False, True], ids=["paged", "dense"])
+def test_prefill_negative_scale(gpu, dense):
+    """A negative softmax scale (folded into the sign of q_rot in the kernel)."""
+    print(f"[prefill] negative scale dense={dense}", flush=True)
+    case = make_prefill_case(4500, [90, 33], [120, 33], H_kv=8, gs=4, scale=-0.15)
+    out = run_prefill(case, gpu, dense=dense, scale=-0.15)
+    check(out, case.expected)
+
+
 @pytest.mark.parametrize("block_size", [32, 48])
 def test_prefill_larger_blocks(gpu, block_size):
     """Pages of 32 and 48 tokens (the block-table entries are fetched one tile
