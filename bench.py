@@ -754,6 +754,7 @@ def main(argv=None):
                 ww = w if (sb, sn) == (B, N) else make_workload(sb, sn, dev)
                 f2 = decode_call(ww)
                 g2 = capture(f2, 5)
+                settle(g2, 0.05)
                 us = replay_median_us(g2, 20)
                 kus = split_kernel_us(f2, 20)
                 nb2 = _native.decode_algorithmic_bytes(sb, sn)

@@ -897,8 +897,8 @@ __device__ __forceinline__ float wave_sum(float v) {
 // Merge split partials (attention.py:239-272: m* = max m_i, weights
 // exp(m_i - m*), empty splits weigh 0, l clamped at 1e-30), round O_rot to
 // fp16 and unrotate: out[j] = sum_k fp16(O_rot)[k] * R[j][k].  One 256-thread
-// block per (4 q-heads, sequence): wave w merges head w (two dims per lane, 16
-// splits' loads in flight at a time).  R is staged in LDS in its own row
+// block per (4 q-heads, sequence): wave w merges head w (two splits per wave
+// instruction, four dims per lane, 32 splits' loads in flight at a time).  R is staged in LDS in its own row
 // order with rows padded to 132 floats, so the global reads are coalesced,
 // all sixteen per thread are in flight at once, and the epilogue's 16-byte
 // row reads (lane j reads row j) fall in distinct banks.
@@ -924,17 +924,27 @@ combine_kernel(const float *part_o, const float *part_ml, const float *R, uint16
     const int64_t base = (int64_t)b * n_splits * H_q + h;
     float L = 0.0f;
     if (live) {
+        // All (m, l) pairs of this head in flight at once (up to kMaxSplits).
+        constexpr int kPer = kMaxSplits / 64;
+        float2 ml[kPer];
+#pragma unroll
+        for (int i = 0; i < kPer; ++i) {
+            const int s = lane + 64 * i;
+            ml[i] = (s < n_splits)
+                        ? *reinterpret_cast<const float2 *>(part_ml + (base + (int64_t)s * H_q) * 2)
+                        : make_float2(-INFINITY, 0.0f);
+        }
         float mx = -INFINITY;
-        for (int s = lane; s < n_splits; s += 64)
-            mx = fmaxf(mx, part_ml[(base + (int64_t)s * H_q) * 2]);
+#pragma unroll
+        for (int i = 0; i < kPer; ++i) mx = fmaxf(mx, ml[i].x);
         mx = wave_max(mx);
         float lp = 0.0f;
-        for (int s = lane; s < n_splits; s += 64) {
-            const int64_t r = base + (int64_t)s * H_q;
-            const float ms = part_ml[r * 2];
-            const float w = (ms == -INFINITY) ? 0.0f : exp2f(ms - mx);
-            wts[hh][s] = w;
-            if (w != 0.0f) lp += w * part_ml[r * 2 + 1];
+#pragma unroll
+        for (int i = 0; i < kPer; ++i) {
+            const int s = lane + 64 * i;
+            const float w = (ml[i].x == -INFINITY) ? 0.0f : exp2f(ml[i].x - mx);
+            if (s < n_splits) wts[hh][s] = w;
+            if (w != 0.0f) lp += w * ml[i].y;
         }
         L = wave_sum(lp);
     }
@@ -946,37 +956,46 @@ combine_kernel(const float *part_o, const float *part_ml, const float *R, uint16
     __syncthreads();
     if (live) {
         // Empty splits store zeros, so every partial is read unconditionally.
-        const float *po = part_o + base * kD + 2 * lane;
+        // Lanes 0-31 take the even splits and lanes 32-63 the odd ones, four
+        // dims per lane, sixteen 16-byte loads in flight: 32 splits per batch.
+        const int half = lane >> 5, d4 = 4 * (lane & 31);
+        const float *po = part_o + base * kD + d4;
         const int64_t step = (int64_t)H_q * kD;
-        float o0 = 0.0f, o1 = 0.0f;
-        int s = 0;
-        for (; s + 16 <= n_splits; s += 16) {
-            float2 v[16];
-#pragma unroll
-            for (int u = 0; u < 16; ++u)
-                v[u] = *reinterpret_cast<const float2 *>(po + (int64_t)(s + u) * step);
+        float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
+        for (int s0 = 0; s0 < n_splits; s0 += 32) {
+            float4 v[16];
 #pragma unroll
             for (int u = 0; u < 16; ++u) {
-                o0 = fmaf(wts[hh][s + u], v[u].x, o0);
-                o1 = fmaf(wts[hh][s + u], v[u].y, o1);
+                const int s = s0 + 2 * u + half;
+                v[u] = (s < n_splits) ? *reinterpret_cast<const float4 *>(po + (int64_t)s * step)
+                                      : make_float4(0.f, 0.f, 0.f, 0.f);
+            }
+#pragma unroll
+            for (int u = 0; u < 16; ++u) {
+                const int s = s0 + 2 * u + half;
+                const float w = (s < n_splits) ? wts[hh][s] : 0.0f;
+                o.x = fmaf(w, v[u].x, o.x);
+                o.y = fmaf(w, v[u].y, o.y);
+                o.z = fmaf(w, v[u].z, o.z);
+                o.w = fmaf(w, v[u].w, o.w);
             }
         }
-        if (s < n_splits) {
-            float2 v[16];
-#pragma unroll
-            for (int u = 0; u < 16; ++u)
-                if (s + u < n_splits)
-                    v[u] = *reinterpret_cast<const float2 *>(po + (int64_t)(s + u) * step);
-#pragma unroll
-            for (int u = 0; u < 16; ++u)
-                if (s + u < n_splits) {
-                    o0 = fmaf(wts[hh][s + u], v[u].x, o0);
-                    o1 = fmaf(wts[hh][s + u], v[u].y, o1);
-                }
-        }
+        auto sum_halves = [](float x) {
+            const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x),
+                                                            false, false);
+            return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+        };
+        o.x = sum_halves(o.x);
+        o.y = sum_halves(o.y);
+        o.z = sum_halves(o.z);
+        o.w = sum_halves(o.w);
         const float inv = 1.0f / fmaxf(L, 1e-30f);
-        orot[hh][2 * lane] = h2f(__half_as_ushort(__float2half_rn(o0 * inv)));
-        orot[hh][2 * lane + 1] = h2f(__half_as_ushort(__float2half_rn(o1 * inv)));
+        if (half == 0) {
+            orot[hh][d4 + 0] = h2f(__half_as_ushort(__float2half_rn(o.x * inv)));
+            orot[hh][d4 + 1] = h2f(__half_as_ushort(__float2half_rn(o.y * inv)));
+            orot[hh][d4 + 2] = h2f(__half_as_ushort(__float2half_rn(o.z * inv)));
+            orot[hh][d4 + 3] = h2f(__half_as_ushort(__float2half_rn(o.w * inv)));
+        }
     }
     __syncthreads();
     if (!live) return;
