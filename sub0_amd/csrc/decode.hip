@@ -47,10 +47,6 @@ constexpr int kChunk = 32;                // tokens per inner iteration (2 MFMA 
 constexpr int kLutDwords = 2 * 256 * 64;
 constexpr float kLog2e = 1.4426950408889634f;
 
-#ifndef CDA_DECODE_DEPTH
-#define CDA_DECODE_DEPTH 2
-#endif
-
 struct SplitParams {
     const uint16_t *q_rot;      // (B, H_q, 128) fp16
     const uint8_t *kv;          // paged cache
@@ -409,27 +405,10 @@ decode_split_kernel(SplitParams p) {
     };
 
     // ---- main loop over the full 32-token chunks; loads run one chunk
-    // ahead (CDA_DECODE_DEPTH 2) or two (3).  A partial last chunk is handled
-    // after the loop, so the loop body carries no masking.
+    // ahead.  A partial last chunk is handled after the loop, so the loop body
+    // carries no masking.
     const int nfull = (end - start) / kChunk;
     int i = 0;
-#if CDA_DECODE_DEPTH == 3
-    Chunk ca, cb, cc;
-    if (nfull > 0) load_chunk(ca, start);
-    if (nfull > 1) load_chunk(cb, start + kChunk);
-#define CDA_STEP(CUR, NEXT2)                                                   \
-    {                                                                          \
-        if (i >= nfull) break;                                                 \
-        if (i + 2 < nfull) load_chunk(NEXT2, start + (i + 2) * kChunk);        \
-        compute_chunk(CUR, start + i * kChunk, std::false_type{});             \
-        ++i;                                                                   \
-    }
-    while (true) {
-        CDA_STEP(ca, cc)
-        CDA_STEP(cb, ca)
-        CDA_STEP(cc, cb)
-    }
-#else
     Chunk ca, cb;
     if (nfull > 0) load_chunk(ca, start);
 #define CDA_STEP(CUR, NEXT)                                                    \
@@ -443,7 +422,6 @@ decode_split_kernel(SplitParams p) {
         CDA_STEP(ca, cb)
         CDA_STEP(cb, ca)
     }
-#endif
 #undef CDA_STEP
     if (start + nfull * kChunk < end) {
         load_chunk(ca, start + nfull * kChunk);
