@@ -65,6 +65,20 @@ def test_invalid_arguments_are_rejected_before_launch():
     assert L.cda_decode_set_timing_events(dummy, None) == -1
 
 
+def test_prefill_arguments_are_rejected_before_launch():
+    from sub0_amd import _native
+    L = _native.lib()
+    P = ctypes.c_void_p
+    d = P(256)
+
+    def call(slot_bytes, block_size, cache=d):
+        return L.cda_prefill_paged_hadamard(d, cache, 64, slot_bytes, 8, d, 4, d, d, 1, d, d, 16,
+                                            d, 8, 32, block_size, 8, 0.1, None)
+    assert call(144, 24) == -1 and b"multiple of 16" in L.cda_hip_last_error()
+    assert call(128, 16) == -1 and b"slot" in L.cda_hip_last_error()
+    assert call(144, 16, P(260)) == -1 and b"aligned" in L.cda_hip_last_error()
+
+
 def test_python_binding_refuses_cpu_tensors():
     import torch
     from sub0_amd import _native
