@@ -139,6 +139,39 @@ def prefill_call(w, dense: bool = False):
     return call
 
 
+def prefill_cpu_baseline(n: int = 1024, reps: int = 3):
+    """The C restatement (oracle/) of the causal prefill on one n-token
+    sequence (32 Q / 8 KV heads) over a paged K4V4 cache."""
+    sys.path.insert(0, str(ROOT))
+    import numpy as np
+    from oracle import cda_oracle as O
+    from oracle import synth
+    cb = np.load(ROOT / "tests" / "golden" / "codebooks.npz")["lloyd_beta16"]
+    W = (n + BS - 1) // BS
+    bt = synth.permuted_block_table(0xCDA3, 1, W)
+    k = synth.kv_with_outliers(0xCDA3, (1, H_KV, n, D))
+    v = synth.normal_f16(0xCDA4, (1, H_KV, n, D))
+    kp, kn, _ = O.encode(k, cb)
+    vp, vn, _ = O.encode(v, cb)
+    cache = O.build_paged_cache(kp, kn, vp, vn, bt, BS, cb.size, num_blocks=W)
+    q = synth.normal_f16(0xCDA5, (n, H_Q, D))
+    cu = np.array([0, n], dtype=np.int32)
+    seq = np.array([n], dtype=np.int32)
+    R = O.hadamard128()
+    nt = min(16, os.cpu_count() or 1)
+    O.set_threads(nt)
+    ts = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        O.prefill_paged(q, cu, cache, bt, seq, cb, cb, R, H_kv=H_KV, block_size=BS)
+        ts.append(time.perf_counter() - t0)
+    sec = statistics.median(ts)
+    flops = 4 * H_Q * D * (n * (n + 1) // 2)
+    return {"value": round(flops / sec / 1e12, 5), "unit": "TFLOP/s", "cores": nt, "kind": "port",
+            "sample": f"one {n}-token causal sequence, 32/8 heads, {sec * 1e3:.0f} ms on {nt} "
+                      f"threads (median of {reps}); the C restatement, float64 accumulation"}
+
+
 def prefill_main(args) -> int:
     """--prefill: BASELINE config 3 (not the headline metric); one JSON line."""
     import torch
@@ -173,6 +206,12 @@ def prefill_main(args) -> int:
                      "kernel": "prefill_kernel<paged>"},
         "dense_bridge_ms": round(res["dense_bridge"], 4),
     }
+    if not args.no_cpu_baseline:
+        try:
+            line["cpu_baseline"] = prefill_cpu_baseline()
+        except Exception as e:  # the baseline is informative only
+            log(f"prefill cpu baseline skipped: {e}")
+            line["cpu_baseline"] = None
     print(json.dumps(line), flush=True)
     return 0
 
