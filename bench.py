@@ -49,10 +49,12 @@ def log(*a):
 
 # --------------------------------------------------------------- workload --
 
-def make_workload(B: int, N: int, dev, seed: int | None = None, identity_bt: bool = False):
-    """Paged K4V4 cache of B sequences x N tokens, encoded on the GPU by the
-    fused encoder from K, V ~ N(0,1) fp16 (K with 4 seeded outlier channels
-    x8), plus q ~ N(0,1); synthetic data."""
+def make_workload(B: int, N: int, dev, seed: int | None = None, identity_bt: bool = False,
+                  levels: int = 16):
+    """Paged K4V4 (levels 16, 144-byte slots) or K2V2 (levels 4, 80-byte
+    slots) cache of B sequences x N tokens, encoded on the GPU by the fused
+    encoder from K, V ~ N(0,1) fp16 (K with 4 seeded outlier channels x8),
+    plus q ~ N(0,1); synthetic data."""
     import torch
     from sub0_amd import _native
     from sub0_amd.cda.algorithm.compression import hadamard_matrix, lloyd_max_centroids_beta
@@ -64,8 +66,9 @@ def make_workload(B: int, N: int, dev, seed: int | None = None, identity_bt: boo
     perm = torch.arange(B * nb) if identity_bt else torch.randperm(B * nb, generator=cpu)
     bt = perm.to(torch.int32).view(B, nb).to(dev)
     outl = torch.randperm(D, generator=cpu)[:4].to(dev)
-    cache = torch.zeros(B * nb * BS, H_KV, 144, dtype=torch.uint8, device=dev)
-    cb = lloyd_max_centroids_beta(16, D).to(dev)
+    cache = torch.zeros(B * nb * BS, H_KV, 144 if levels == 16 else 80, dtype=torch.uint8,
+                        device=dev)
+    cb = lloyd_max_centroids_beta(levels, D).to(dev)
     chunk = 1 << 16                                    # tokens per encode launch
     pos = torch.arange(N, device=dev, dtype=torch.int64)
     for b in range(B):
@@ -727,6 +730,8 @@ def main(argv=None):
     ap.add_argument("--e2e-batch", type=int, default=32)
     ap.add_argument("--e2e-prefix", type=int, default=16384)
     ap.add_argument("--e2e-steps", type=int, default=256)
+    ap.add_argument("--k2v2", action="store_true",
+                    help="decode over a K2V2 cache (4-level codebook, 80-byte slots) instead of K4V4")
     ap.add_argument("--general-kernel", action="store_true",
                     help="forbid the page-streaming split kernel (A/B diagnostic)")
     ap.add_argument("--identity-block-table", action="store_true",
@@ -764,7 +769,8 @@ def main(argv=None):
         _native.set_stream_kernel(False)
     B, N = args.B, args.N
 
-    w = make_workload(B, N, dev, identity_bt=args.identity_block_table)
+    levels = 4 if args.k2v2 else 16
+    w = make_workload(B, N, dev, identity_bt=args.identity_block_table, levels=levels)
     fn = decode_call(w, args.tile_n)
     g = capture(fn, args.warmup)
     settle(g)
@@ -779,7 +785,8 @@ def main(argv=None):
     ms_per_step = (t1 - t0) / args.steps * 1e3
     med_us = replay_median_us(g, 20)
     k_us = split_kernel_us(fn, max(5, args.steps))
-    nbytes = _native.decode_algorithmic_bytes(B, N)
+    slot_data = 136 if levels == 16 else 72
+    nbytes = _native.decode_algorithmic_bytes(B, N, slot_data=slot_data)
     value = nbytes / (ms_per_step * 1e-3) / 1e9
     achieved = nbytes / (k_us * 1e-6) / 1e9
     tile, splits = _native.decode_plan(B, H_Q, H_KV, N, args.tile_n)
@@ -813,7 +820,7 @@ def main(argv=None):
             Path(args.sweep_out).write_text(json.dumps(sweep, indent=1) + "\n")
 
     cpu = None
-    if not args.no_cpu_baseline:
+    if not args.no_cpu_baseline and levels == 16:   # the CPU baseline is the K4V4 config 0
         try:
             cpu = cpu_baseline()
         except Exception as e:  # the baseline is reported, never required
@@ -821,8 +828,11 @@ def main(argv=None):
 
     # The workload (8 KV heads, 144-byte slots, one codebook) is eligible for
     # the page-streaming kernel unless it is switched off.
+    # Both code widths (8 KV heads, one codebook) take the page-streaming kernel
+    # unless it is switched off.
     kernel = "decode_split_kernel" if args.general_kernel else "decode_stream_kernel"
-    traffic = load_traffic(kernel, B, N)
+    traffic = load_traffic(kernel, B, N) if levels == 16 else None
+    variant = "K4V4" if levels == 16 else "K2V2"
     line = {
         "metric": METRIC,
         "value": round(value, 1),
@@ -837,10 +847,10 @@ def main(argv=None):
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "u4 codes, fp16 MFMA operands, fp32 accumulate",
+        "dtype": f"u{2 if levels == 4 else 4} codes, fp16 MFMA operands, fp32 accumulate",
         "data": "synthetic (K,V,q ~ N(0,1) fp16, K with 4 outlier channels x8, "
-                "Lloyd-beta 16-level codebook, permuted block table)",
-        "config": {"workload": f"K4V4 paged decode, B={B}, N={N}, Llama-3-8B heads "
+                f"Lloyd-beta {levels}-level codebook, permuted block table)",
+        "config": {"workload": f"{variant} paged decode, B={B}, N={N}, Llama-3-8B heads "
                                "(32 Q / 8 KV, d=128), block 16",
                    "B": B, "N": N, "H_q": H_Q, "H_kv": H_KV, "head_dim": D, "block_size": BS,
                    "tile_n": tile, "splits": splits, "algorithmic_bytes": nbytes},

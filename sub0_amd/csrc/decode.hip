@@ -446,9 +446,10 @@ decode_split_kernel(SplitParams p) {
 }
 
 // ---------------------------------------------------------------------------
-// Page-streaming split kernel for the common cache shape: 8 KV heads x
-// 144-byte slots, a block size that is a multiple of 16 and one codebook for
-// K and V.
+// Page-streaming split kernel for the common cache shapes: 8 KV heads x
+// 144-byte K4V4 slots (L = 16) or 80-byte K2V2 slots (L = 4), a block size
+// that is a multiple of 16 and one codebook for K and V.  The K4V4 layout is
+// described first; the K2V2 differences follow.
 //
 // Wave h (one per KV head) streams its head's share of each 16-token page
 // (16 x 144 B = 2304 B) into a private 4-page LDS ring with the gfx950
@@ -468,11 +469,20 @@ decode_split_kernel(SplitParams p) {
 // One dequant table serves K and V: row e (256 B) holds (cb[e >> 4],
 // cb[e & 15]) in fp32 for 32 lane columns, read with one ds_read_b64 per code
 // byte.
+//
+// K2V2 (1280 B per head and page, two DMA instructions):
+//   [0, 512)      K codes: piece 16*c + t = token t, 16-byte column c (0..1)
+//   [512, 1024)   V codes: token t's 32 bytes at 32 * vslot2(t)
+//   [1024, 1280)  norms, as above
+// The table row e holds (cb[e >> 6], cb[(e >> 4) & 3]): the code pair in the
+// high nibble of e.  A byte of 2-bit codes (dims 4j..4j+3, first dim in bits
+// 7:6) gives dims (4j, 4j+1) from itself and (4j+2, 4j+3) from the same byte
+// of the word shifted left by 4.  For V, two tokens' codes of one dim are
+// first interleaved into one nibble (bit-field inserts), as the K4V4 path
+// pairs two tokens' nibbles into one byte.
 // ---------------------------------------------------------------------------
 
-constexpr int kStreamRowBytes = 8 * 144;
-constexpr int kPageBytes = 16 * kStreamRowBytes;          // one 16-token page, all heads
-constexpr int kHeadPage = 16 * 144;                        // one head's share: 2304 B
+constexpr int kHeadPage = 16 * 144;      // largest share of one head in a page (K4V4): 2304 B
 
 template <int N>
 using IC = std::integral_constant<int, N>;
@@ -513,10 +523,28 @@ constexpr int kStreamRingOff = kLut2Bytes;
 constexpr int kStreamPidOff = kStreamRingOff + kWaves * kStreamPages * kHeadPage;
 constexpr int kStreamLds = kStreamPidOff + kStreamMaxPages * 4;           // 143360 B
 
-template <int GS>
+// K2V2 V slot of token t: the four tokens read together (4*q4 + i, q4 =
+// 0..3) land in four consecutive 32-byte slots (an involution).
+__host__ __device__ constexpr int vslot2(int t) { return ((t & 3) << 2) | (t >> 2); }
+
+// Bit-field insert: bits of a where m is set, of b elsewhere (v_bfi_b32).
+__device__ __forceinline__ uint32_t bfi(uint32_t m, uint32_t a, uint32_t b) {
+    return (m & a) | (~m & b);
+}
+
+template <int GS, int L>
 __global__ void __launch_bounds__(kThreads, 1)
 decode_stream_kernel(SplitParams p) {
+    static_assert(L == 16 || L == 4, "4-bit or 2-bit codes");
     __shared__ __align__(16) uint8_t smem[kStreamLds];
+    constexpr int S = (L == 16) ? 144 : 80;        // slot bytes
+    constexpr int KB = (L == 16) ? 64 : 32;        // code bytes per role
+    constexpr int kRow = 8 * S;                    // one token row, all heads
+    constexpr int kPB = 16 * kRow;                 // one 16-token page, all heads
+    constexpr int kHP = 16 * S;                    // one head's share of a page
+    constexpr uint32_t kVo = 16 * KB;              // V codes within a ring page
+    constexpr uint32_t kNo = 32 * KB;              // norms within a ring page
+    static_assert(kWaves * kStreamPages * kHP + kStreamRingOff <= kStreamPidOff, "ring fits");
 
     const int sp = blockIdx.x;
     const int b = blockIdx.z;
@@ -541,15 +569,25 @@ decode_stream_kernel(SplitParams p) {
         return;
     }
 
+    // Source offset of lane's 16-byte piece within the head's page rows.
     uint32_t src[3];
-    src[0] = (uint32_t)((lane & 15) * kStreamRowBytes + (lane >> 4) * 16);
-    src[1] = (uint32_t)(vslot_inv(lane >> 2) * kStreamRowBytes + 64 + (lane & 3) * 16);
-    src[2] = (uint32_t)((lane & 15) * kStreamRowBytes + 128);   // lanes 0..15 only
+    if constexpr (L == 16) {
+        src[0] = (uint32_t)((lane & 15) * kRow + (lane >> 4) * 16);
+        src[1] = (uint32_t)(vslot_inv(lane >> 2) * kRow + KB + (lane & 3) * 16);
+        src[2] = (uint32_t)((lane & 15) * kRow + 2 * KB);   // lanes 0..15 only
+    } else {
+        // lanes 0..31: K pieces; lanes 32..63: V pieces (LDS 512 + 16*(lane-32)).
+        const int j = lane & 31;
+        src[0] = (lane < 32) ? (uint32_t)((j & 15) * kRow + (j >> 4) * 16)
+                             : (uint32_t)(vslot2(j >> 1) * kRow + KB + (j & 1) * 16);
+        src[2] = (uint32_t)((lane & 15) * kRow + 2 * KB);   // lanes 0..15 only
+        src[1] = 0;
+    }
 
     const int bs = p.block_size;
     const int npages = (end - start + 15) >> 4;
     const uint32_t ring_w = __builtin_amdgcn_readfirstlane(lds_u32addr(smem)) + kStreamRingOff +
-                            wave * (kStreamPages * kHeadPage);
+                            wave * (kStreamPages * kHP);
     int32_t *page_row = reinterpret_cast<int32_t *>(smem + kStreamPidOff);
     {
         const int32_t *bt = p.block_table + (int64_t)b * p.bt_stride;
@@ -558,18 +596,18 @@ decode_stream_kernel(SplitParams p) {
             page_row[t] = bt[t0 / bs] * bs + (t0 % bs);
         }
     }
-    const uint8_t *kv_h = p.kv + h * 144;
+    const uint8_t *kv_h = p.kv + h * S;
     // DMA of page t into ring slot k.
     auto issue = [&](int t, int k) CDA_INLINE {
         const int64_t row0 = __builtin_amdgcn_readfirstlane(page_row[t]);
-        const uint64_t base = (uint64_t)(kv_h + row0 * kStreamRowBytes);
+        const uint64_t base = (uint64_t)(kv_h + row0 * kRow);
         const v4u32 r = {(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)base),
                          (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(base >> 32) & 0xFFFFu),
-                         (uint32_t)(kPageBytes - h * 144), 0x00020000u};
-        const uint32_t sb = ring_w + (uint32_t)k * kHeadPage;
+                         (uint32_t)(kPB - h * S), 0x00020000u};
+        const uint32_t sb = ring_w + (uint32_t)k * kHP;
         dma_page_chunk(r, src[0], sb);
-        dma_page_chunk(r, src[1], sb + 1024);
-        if (lane < 16) dma_page_chunk(r, src[2], sb + 2048);
+        if constexpr (L == 16) dma_page_chunk(r, src[1], sb + kVo);
+        if (lane < 16) dma_page_chunk(r, src[2], sb + kNo);
     };
     uint4 qb[4];
     {
@@ -583,12 +621,15 @@ decode_stream_kernel(SplitParams p) {
         // would put 32 dependent memory round trips in every thread's
         // prologue.
         __shared__ float cbs[16];
-        if (tid < 16) cbs[tid] = p.cb_k[tid];
+        if (tid < L) cbs[tid] = p.cb_k[tid];
         __syncthreads();
         uint32_t *lut = reinterpret_cast<uint32_t *>(smem);
         for (int i = tid; i < kLut2Bytes / 4; i += kThreads) {
             const int e = i >> 6;
-            lut[i] = __float_as_uint(cbs[(i & 1) ? (e & 15) : (e >> 4)]);
+            if constexpr (L == 16)
+                lut[i] = __float_as_uint(cbs[(i & 1) ? (e & 15) : (e >> 4)]);
+            else
+                lut[i] = __float_as_uint(cbs[(i & 1) ? ((e >> 4) & 3) : (e >> 6)]);
         }
     }
     __syncthreads();
@@ -598,14 +639,17 @@ decode_stream_kernel(SplitParams p) {
     for (int k = 0; k < kStreamPages; ++k)
         if (k < npages) issue(k, k);
 
-    const uint32_t rb0 = (uint32_t)(kStreamRingOff + wave * (kStreamPages * kHeadPage));
-    const uint32_t oK = rb0 + (uint32_t)lane * 16u;
-    const uint32_t oNK = rb0 + 2048u + 16u * r16;
+    const uint32_t rb0 = (uint32_t)(kStreamRingOff + wave * (kStreamPages * kHP));
+    // K4V4: token r16's 16 code bytes of dims [32*q4, +32); K2V2: its 8 bytes.
+    const uint32_t oK = (L == 16) ? rb0 + (uint32_t)lane * 16u
+                                  : rb0 + 256u * (q4 >> 1) + 16u * r16 + 8u * (q4 & 1);
+    const uint32_t oNK = rb0 + kNo + 16u * r16;
     uint32_t oV[4], oNV[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        oV[i] = rb0 + 1024u + 64u * vslot(4 * q4 + i) + 4u * r16;
-        oNV[i] = rb0 + 2048u + 16u * (4 * q4 + i) + 4u;
+        oV[i] = (L == 16) ? rb0 + kVo + 64u * vslot(4 * q4 + i) + 4u * r16
+                          : rb0 + kVo + 32u * vslot2(4 * q4 + i) + 2u * r16;
+        oNV[i] = rb0 + kNo + 16u * (4 * q4 + i) + 4u;
     }
     const uint32_t col = (uint32_t)(lane & 31) * 8u;
     const uint8_t *lutb = smem;
@@ -624,24 +668,50 @@ decode_stream_kernel(SplitParams p) {
         float nv[4];
     };
     auto read_page = [&](PageRegs &r, auto slot) CDA_INLINE {
-        constexpr uint32_t so = decltype(slot)::value * kHeadPage;
-        r.kq = *reinterpret_cast<const uint4 *>(smem + oK + so);
+        constexpr uint32_t so = decltype(slot)::value * kHP;
+        if constexpr (L == 16) {
+            r.kq = *reinterpret_cast<const uint4 *>(smem + oK + so);
+        } else {
+            const uint2 k2 = *reinterpret_cast<const uint2 *>(smem + oK + so);
+            r.kq = make_uint4(k2.x, k2.y, 0u, 0u);
+        }
         r.nk = __uint_as_float(lds_b32(smem + so, oNK));
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
-            r.vw[k] = lds_b32(smem + so, oV[k]);
+            if constexpr (L == 16)
+                r.vw[k] = lds_b32(smem + so, oV[k]);
+            else
+                r.vw[k] = *reinterpret_cast<const uint16_t *>(smem + so + oV[k]);
             r.nv[k] = __uint_as_float(lds_b32(smem + so, oNV[k]));
         }
     };
     auto page_scores = [&](const PageRegs &r) CDA_INLINE -> floatx4 {
-        const uint32_t w[4] = {r.kq.x, r.kq.y, r.kq.z, r.kq.w};
         float2 cv[16];
+        if constexpr (L == 16) {
+            const uint32_t w[4] = {r.kq.x, r.kq.y, r.kq.z, r.kq.w};
 #pragma unroll
-        for (int s = 0; s < 4; ++s) {
-            cv[4 * s + 0] = CDA_PAIR(0, w[s]);
-            cv[4 * s + 1] = CDA_PAIR(1, w[s]);
-            cv[4 * s + 2] = CDA_PAIR(2, w[s]);
-            cv[4 * s + 3] = CDA_PAIR(3, w[s]);
+            for (int s = 0; s < 4; ++s) {
+                cv[4 * s + 0] = CDA_PAIR(0, w[s]);
+                cv[4 * s + 1] = CDA_PAIR(1, w[s]);
+                cv[4 * s + 2] = CDA_PAIR(2, w[s]);
+                cv[4 * s + 3] = CDA_PAIR(3, w[s]);
+            }
+        } else {
+            // Word x holds dims [16x, 16x+16) of the lane's 32; MFMA s takes
+            // bytes 2s, 2s+1 (dims 8s..8s+7).
+            const uint32_t w[2] = {r.kq.x, r.kq.y};
+            const uint32_t sh[2] = {r.kq.x << 4, r.kq.y << 4};
+#pragma unroll
+            for (int x = 0; x < 2; ++x) {
+                cv[8 * x + 0] = CDA_PAIR(0, w[x]);
+                cv[8 * x + 1] = CDA_PAIR(0, sh[x]);
+                cv[8 * x + 2] = CDA_PAIR(1, w[x]);
+                cv[8 * x + 3] = CDA_PAIR(1, sh[x]);
+                cv[8 * x + 4] = CDA_PAIR(2, w[x]);
+                cv[8 * x + 5] = CDA_PAIR(2, sh[x]);
+                cv[8 * x + 6] = CDA_PAIR(3, w[x]);
+                cv[8 * x + 7] = CDA_PAIR(3, sh[x]);
+            }
         }
         const float nk = r.nk;
         floatx4 acc = {0.f, 0.f, 0.f, 0.f};
@@ -659,27 +729,52 @@ decode_stream_kernel(SplitParams p) {
     // O += P V over pages ra, rb (k slots as in decode_stream_kernel).
     auto pv_pair = [&](const uint4 &pa, const PageRegs &ra, const PageRegs &rb) CDA_INLINE {
         uint32_t ev[4], od[4];
-#pragma unroll
-        for (int m2 = 0; m2 < 2; ++m2) {
-            ev[m2] = (ra.vw[2 * m2] & 0xF0F0F0F0u) | ((ra.vw[2 * m2 + 1] >> 4) & 0x0F0F0F0Fu);
-            od[m2] = ((ra.vw[2 * m2] << 4) & 0xF0F0F0F0u) | (ra.vw[2 * m2 + 1] & 0x0F0F0F0Fu);
-            ev[2 + m2] = (rb.vw[2 * m2] & 0xF0F0F0F0u) | ((rb.vw[2 * m2 + 1] >> 4) & 0x0F0F0F0Fu);
-            od[2 + m2] = ((rb.vw[2 * m2] << 4) & 0xF0F0F0F0u) | (rb.vw[2 * m2 + 1] & 0x0F0F0F0Fu);
-        }
         float2 vc[32];
 #define CDA_V_TILE(K_, SRC_, J_)                                               \
     vc[4 * (J_) + 0] = CDA_PAIR(K_, SRC_[0]);                                  \
     vc[4 * (J_) + 1] = CDA_PAIR(K_, SRC_[1]);                                  \
     vc[4 * (J_) + 2] = CDA_PAIR(K_, SRC_[2]);                                  \
     vc[4 * (J_) + 3] = CDA_PAIR(K_, SRC_[3]);
-        CDA_V_TILE(0, ev, 0)
-        CDA_V_TILE(0, od, 1)
-        CDA_V_TILE(1, ev, 2)
-        CDA_V_TILE(1, od, 3)
-        CDA_V_TILE(2, ev, 4)
-        CDA_V_TILE(2, od, 5)
-        CDA_V_TILE(3, ev, 6)
-        CDA_V_TILE(3, od, 7)
+        if constexpr (L == 16) {
+#pragma unroll
+            for (int m2 = 0; m2 < 2; ++m2) {
+                ev[m2] = (ra.vw[2 * m2] & 0xF0F0F0F0u) | ((ra.vw[2 * m2 + 1] >> 4) & 0x0F0F0F0Fu);
+                od[m2] = ((ra.vw[2 * m2] << 4) & 0xF0F0F0F0u) | (ra.vw[2 * m2 + 1] & 0x0F0F0F0Fu);
+                ev[2 + m2] = (rb.vw[2 * m2] & 0xF0F0F0F0u) | ((rb.vw[2 * m2 + 1] >> 4) & 0x0F0F0F0Fu);
+                od[2 + m2] = ((rb.vw[2 * m2] << 4) & 0xF0F0F0F0u) | (rb.vw[2 * m2 + 1] & 0x0F0F0F0Fu);
+            }
+            CDA_V_TILE(0, ev, 0)
+            CDA_V_TILE(0, od, 1)
+            CDA_V_TILE(1, ev, 2)
+            CDA_V_TILE(1, od, 3)
+            CDA_V_TILE(2, ev, 4)
+            CDA_V_TILE(2, od, 5)
+            CDA_V_TILE(3, ev, 6)
+            CDA_V_TILE(3, od, 7)
+        } else {
+            // Tokens a = 2*m2, b = 2*m2 + 1 (16 bits each: dims 8*r16 .. +7).
+            // t's nibbles pair (a, b) codes of dims 0, 2 | 4, 6 (bytes 0 | 1),
+            // u's of dims 1, 3 | 5, 7; ev = t | (t << 20) puts the dims 2, 6
+            // nibbles high in bytes 2, 3 (od likewise for u).  Bytes of
+            // ev: dims 0, 4, 2, 6; of od: dims 1, 5, 3, 7.
+#pragma unroll
+            for (int x = 0; x < 4; ++x) {
+                const PageRegs &rr = (x < 2) ? ra : rb;
+                const uint32_t a = rr.vw[2 * (x & 1)], bb = rr.vw[2 * (x & 1) + 1];
+                const uint32_t t = bfi(0xCCCCu, a, bb >> 2);
+                const uint32_t u = bfi(0xCCCCu, a << 2, bb);
+                ev[x] = t | (t << 20);
+                od[x] = u | (u << 20);
+            }
+            CDA_V_TILE(0, ev, 0)
+            CDA_V_TILE(0, od, 1)
+            CDA_V_TILE(2, ev, 2)
+            CDA_V_TILE(2, od, 3)
+            CDA_V_TILE(1, ev, 4)
+            CDA_V_TILE(1, od, 5)
+            CDA_V_TILE(3, ev, 6)
+            CDA_V_TILE(3, od, 7)
+        }
 #undef CDA_V_TILE
         // V rebuilt exactly as the reference decodes it: fp16(centroid * norm)
         // per element (k slot pairs are two tokens of one dim).
@@ -1154,16 +1249,23 @@ extern "C" int cda_decode_full_hmma_v3(const void *q, const void *kv_cache, int6
     // The page-streaming kernel covers 8 KV heads x 144-byte slots with one
     // codebook for K and V (passed as the same pointer) and splits of at most
     // 1024 pages; anything else takes the general kernel.
-    const bool use_stream = levels == 16 && H_kv == 8 && slot_bytes == kStreamRowBytes / 8 &&
+    const bool use_stream = H_kv == 8 &&
+                            ((levels == 16 && slot_bytes == 144) ||
+                             (levels == 4 && slot_bytes == 80)) &&
                             cb_k == cb_v &&
                             tn <= 16 * kStreamMaxPages && g_allow_stream;
     if (g_split_start && hipEventRecord(g_split_start, st) != hipSuccess)
         return fail(CDA_E_HIP, "cda_decode_full_hmma_v3: hipEventRecord(start) failed");
-    if (use_stream) {
+    if (use_stream && levels == 16) {
         if (group_size == 4)
-            decode_stream_kernel<4><<<grid, kThreads, 0, st>>>(p);
+            decode_stream_kernel<4, 16><<<grid, kThreads, 0, st>>>(p);
         else
-            decode_stream_kernel<8><<<grid, kThreads, 0, st>>>(p);
+            decode_stream_kernel<8, 16><<<grid, kThreads, 0, st>>>(p);
+    } else if (use_stream) {
+        if (group_size == 4)
+            decode_stream_kernel<4, 4><<<grid, kThreads, 0, st>>>(p);
+        else
+            decode_stream_kernel<8, 4><<<grid, kThreads, 0, st>>>(p);
     } else if (levels == 4) {
         if (group_size == 4)
             decode_split_kernel<4, 4><<<grid, kThreads, 0, st>>>(p);

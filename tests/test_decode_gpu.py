@@ -106,23 +106,36 @@ def test_decode_short_sequences(gpu, seed, seq_lens):
 
 
 K2V2_CASES = [
-    # name, seq_lens, gs, tile_n, fill
-    ("k2v2_ragged", [300, 1, 77, 1031], 4, 0, 0xFF),
-    ("k2v2_gs8", [500, 1200], 8, 0, 0),
-    ("k2v2_tile64", [2000], 4, 64, 0xFF),
+    # name, seq_lens, gs, block_size, tile_n, fill
+    ("k2v2_ragged", [300, 1, 77, 1031], 4, 16, 0, 0xFF),
+    ("k2v2_gs8", [500, 1200], 8, 16, 0, 0),
+    ("k2v2_tile64", [2000], 4, 16, 64, 0xFF),
+    ("k2v2_short", [1, 2, 3, 5, 9, 17, 65], 4, 16, 0, 0xFF),
+    ("k2v2_block32", [999, 64], 4, 32, 0, 0xFF),
 ]
 
 
-@pytest.mark.parametrize("name,seq_lens,gs,tile_n,fill", K2V2_CASES, ids=[c[0] for c in K2V2_CASES])
-def test_decode_k2v2_matches_checker(gpu, codebooks, name, seq_lens, gs, tile_n, fill):
+@pytest.mark.parametrize("name,seq_lens,gs,bs,tile_n,fill", K2V2_CASES,
+                         ids=[c[0] for c in K2V2_CASES])
+def test_decode_k2v2_matches_checker(gpu, codebooks, name, seq_lens, gs, bs, tile_n, fill):
     """2-bit K and V codes (4-level codebook, 80-byte slots; pack_2bit,
-    compression.py:375-397) through the general kernel."""
-    print(f"[decode-k2v2] case={name} seq_lens={seq_lens} gs={gs}", flush=True)
+    compression.py:375-397) through the page-streaming kernel (8 KV heads, one
+    codebook) and the general kernel; both meet the bar and agree."""
+    from sub0_amd import _native
+    print(f"[decode-k2v2] case={name} seq_lens={seq_lens} gs={gs} bs={bs}", flush=True)
     cb4 = codebooks["lloyd_beta4"].astype(np.float32)
-    case = make_decode_case(5000 + len(name), seq_lens, H_kv=8, gs=gs, cb=cb4, fill=fill)
+    case = make_decode_case(5000 + len(name), seq_lens, H_kv=8, gs=gs, block_size=bs, cb=cb4,
+                            fill=fill)
     assert case.cache.shape[-1] == 80
-    out = run_gpu_decode(case, gpu, gs=gs, tile_n=tile_n)
-    check(out, case.expected)
+    streamed = run_gpu_decode(case, gpu, gs=gs, tile_n=tile_n)
+    check(streamed, case.expected)
+    _native.set_stream_kernel(False)
+    try:
+        general = run_gpu_decode(case, gpu, gs=gs, tile_n=tile_n)
+    finally:
+        _native.set_stream_kernel(True)
+    check(general, case.expected)
+    check(streamed, general, tol=1e-3)
 
 
 def test_decode_k2v2_separate_codebooks(gpu, codebooks):
