@@ -1,8 +1,8 @@
 """Parity at the benchmark's full sizes, against plain PyTorch references on
 the GPU built from the dense dequantised cache (paged_to_dense, itself
 bit-exact against the checker): the BASELINE config-1 headline cell
-(B=32, N=65536) for decode on both split kernels, and the config-3 draw for
-prefill.  The references follow the checker's arithmetic: q_rot rounded to
+(B=32, N=65536) for decode on both split kernels (and K2V2 on the
+page-streaming kernel), and the config-3 draw for prefill.  The references follow the checker's arithmetic: q_rot rounded to
 fp16, scores/softmax/PV in float64 (decode) or float32 (prefill) on the fp16
 K/V rows, O_rot rounded to fp16, then the inverse rotation rounded to fp16."""
 import pytest
@@ -50,6 +50,54 @@ def test_decode_fullsize_against_torch(gpu, stream):
     assert torch.isfinite(out).all()
     err = (out.float() - ref.float()).abs().max().item()
     print(f"[fullsize] decode max abs err {err:.3e}", flush=True)
+    assert err <= TOL
+
+
+def _k2v2_dense(w, b):
+    """Rows of sequence b of a K2V2 cache (80-byte slots: 32 K code bytes, 32 V
+    code bytes, fp32 Kn, fp32 Vn) decoded as fp16(centroid * norm), dim 4j in
+    bits 7:6 of byte j (compression.py:355-359, 375-397)."""
+    N = w["N"]
+    t = torch.arange(N, device=w["q"].device)
+    slots = w["bt"][b, t // BS].long() * BS + t % BS
+    rows = w["cache"][slots]                                        # (N, 8, 80) u8
+    shifts = torch.tensor([6, 4, 2, 0], device=rows.device, dtype=torch.uint8)
+
+    def unpack(x):                                                  # (N, 8, 32) -> (N, 8, 128)
+        return ((x.unsqueeze(-1) >> shifts) & 3).reshape(*x.shape[:-1], 128).long()
+
+    kn = rows[..., 64:68].contiguous().view(torch.float32)          # (N, 8, 1)
+    vn = rows[..., 68:72].contiguous().view(torch.float32)
+    cb = w["cb"].float()
+    K = (cb[unpack(rows[..., :32])] * kn).half()
+    V = (cb[unpack(rows[..., 32:64])] * vn).half()
+    return K, V
+
+
+def test_decode_k2v2_fullsize_against_torch(gpu):
+    """K2V2 (4-level codebook, 80-byte slots) at B=32, N=65536 on the
+    page-streaming kernel."""
+    import bench
+    print("[fullsize] K2V2 decode B=32 N=65536", flush=True)
+    w = bench.make_workload(32, 65536, gpu, levels=4)
+    assert w["cache"].shape[-1] == 80
+    bench.decode_call(w)()
+    torch.cuda.synchronize()
+    R = w["R"].double()
+    q_rot = (w["q"].double() @ R).float().half().double()
+    ref = torch.empty_like(w["out"])
+    for b in range(w["B"]):
+        K, V = _k2v2_dense(w, b)
+        for h in range(H_KV):
+            qh = q_rot[b, 4 * h:4 * h + 4]
+            s = (qh @ K[:, h].double().T) / D ** 0.5
+            p = torch.softmax(s, dim=-1)
+            o_rot = (p @ V[:, h].double()).float().half().double()
+            ref[b, 4 * h:4 * h + 4] = (o_rot @ R.T).float().half()
+    out = w["out"]
+    assert torch.isfinite(out).all()
+    err = (out.float() - ref.float()).abs().max().item()
+    print(f"[fullsize] K2V2 decode max abs err {err:.3e}", flush=True)
     assert err <= TOL
 
 
