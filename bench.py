@@ -130,15 +130,25 @@ def make_prefill_workload(dev, seed: int = 0xCDA3, n_seq: int = 8, lo: int = 512
                 out=torch.empty_like(q), lens=lens, T=T, flops=flops)
 
 
-def prefill_call(w, dense: bool = False):
+def prefill_call(w, source: str = "auto"):
+    """One fa2_cda_prefill_varlen_v1 call over the workload; `source` is the
+    CDA_PREFILL_SOURCE in force while the call runs (auto, compressed, dense)."""
     from sub0_amd.cda.kernels_cuda.fa2_cda import fa2_cda_prefill_varlen_v1
 
     def call():
-        fa2_cda_prefill_varlen_v1(w["q"], w["cache"], w["bt"], w["cu"], w["seq"], w["out"],
-                                  cb_K=w["cb"], cb_V=w["cb"], rotation_fp32=w["R"],
-                                  group_size=H_Q // H_KV, block_size=BS,
-                                  max_query_len=max(w["lens"]), max_seq_len=max(w["lens"]),
-                                  fuse_fa2_epilogue=True, return_dense_kv=dense)
+        old = os.environ.get("CDA_PREFILL_SOURCE")
+        os.environ["CDA_PREFILL_SOURCE"] = source
+        try:
+            fa2_cda_prefill_varlen_v1(w["q"], w["cache"], w["bt"], w["cu"], w["seq"], w["out"],
+                                      cb_K=w["cb"], cb_V=w["cb"], rotation_fp32=w["R"],
+                                      group_size=H_Q // H_KV, block_size=BS,
+                                      max_query_len=max(w["lens"]), max_seq_len=max(w["lens"]),
+                                      fuse_fa2_epilogue=True)
+        finally:
+            if old is None:
+                os.environ.pop("CDA_PREFILL_SOURCE", None)
+            else:
+                os.environ["CDA_PREFILL_SOURCE"] = old
     return call
 
 
@@ -180,9 +190,11 @@ def prefill_main(args) -> int:
     import torch
     dev = torch.device("cuda:0")
     w = make_prefill_workload(dev)
+    from sub0_amd.cda.kernels_cuda.fa2_cda import prefill_source
+    chosen = prefill_source(len(w["lens"]), H_KV, max(w["lens"]), max(w["lens"]))
     res = {}
-    for name, dense in (("compressed_tiles", False), ("dense_bridge", True)):
-        g = capture(prefill_call(w, dense), args.warmup)
+    for name, src in (("compressed_tiles", "compressed"), ("dense_bridge", "dense")):
+        g = capture(prefill_call(w, src), args.warmup)
         settle(g)
         for _ in range(args.warmup):
             g.replay()
@@ -193,7 +205,8 @@ def prefill_main(args) -> int:
         torch.cuda.synchronize()
         res[name] = (time.perf_counter() - t0) / args.steps * 1e3
         del g
-    ms = res["compressed_tiles"]
+    # The default (auto) source is the one measured for `value`.
+    ms = res["dense_bridge" if chosen == "dense" else "compressed_tiles"]
     tflops = w["flops"] / (ms * 1e-3) / 1e12
     peak = 2500.0
     line = {
@@ -206,7 +219,10 @@ def prefill_main(args) -> int:
                    "lengths": w["lens"], "tokens": w["T"], "flops": w["flops"]},
         "roofline": {"bound": "mfma", "achieved": round(tflops, 1), "peak": peak,
                      "unit": "TFLOP/s", "frac": round(tflops / peak, 4),
-                     "kernel": "prefill_kernel<paged>"},
+                     "kernel": "prefill_kernel<dense> + paged_to_dense_kernel" if chosen == "dense"
+                     else "prefill_kernel<paged>"},
+        "prefill_source": chosen,
+        "compressed_tiles_ms": round(res["compressed_tiles"], 4),
         "dense_bridge_ms": round(res["dense_bridge"], 4),
     }
     if not args.no_cpu_baseline:

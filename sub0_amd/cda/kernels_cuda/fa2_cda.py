@@ -1,19 +1,33 @@
 """CDA prefill (drop-in for ``cda/kernels_cuda/fa2_cda.py``).
 
 Same public functions and argument handling as the reference
-(``fa2_cda.py:36-230``).  On MI355X the fused path
-(``fuse_fa2_epilogue=True``) does not materialise dense K/V in HBM: one
-kernel dequantises 64-key tiles of the compressed paged cache into LDS and
-runs a causal flash attention on MFMA with the Hadamard rotation of Q in
-front and the inverse rotation of O behind.  With ``return_dense_kv=True``
-the dense rotated K/V are materialised (the reference's stage-0 bridge) and
-the same attention runs over them.  The unfused path of the reference calls
-vLLM's FlashAttention around two Hadamard transforms; here it computes the
-same quantity (fp16 q_rot, fp16 O_rot, fp16 output) with the fused kernel.
+(``fa2_cda.py:36-230``).  One causal flash-attention kernel on MFMA, with the
+Hadamard rotation of Q in front and the inverse rotation of O behind, reads
+its K/V tiles from one of two sources:
+
+* compressed: 64-key tiles of the paged cache dequantised straight into LDS
+  (no dense K/V in HBM);
+* dense: the rotated fp16 K/V materialised first (the reference's stage-0
+  bridge, ``paged_cache_to_dense_rotated``), then read as plain rows.
+
+The dense bridge dequantises every key once, the compressed source once per
+64-query block, so long query chunks favour the bridge and short ones (chunked
+prefill over a long past) the compressed tiles.  Measured on MI355X (eager,
+32/8 heads): 8 sequences of 2K-7.6K new tokens 2.57 ms compressed / 2.25 ms
+dense; 512-query chunks over 5K-8K keys 0.70 / 0.64; 2048-query chunks over
+16K keys 2.89 / 2.52; 64-query chunks over 4K keys 0.21 / 0.36; 16 queries
+over 16K keys 0.49 / 0.69; 64 sequences of 64-256 tokens 0.14 / 0.15.  The
+default (``CDA_PREFILL_SOURCE=auto``) takes the bridge when max_query_len >=
+256 and the dense K/V fit in 4 GiB; ``compressed`` / ``dense`` force a
+source.  ``return_dense_kv=True`` always takes the bridge and returns the
+dense K/V.  The unfused path of the reference calls vLLM's FlashAttention
+around two Hadamard transforms; here it computes the same quantity (fp16
+q_rot, fp16 O_rot, fp16 output) with the same kernel.
 """
 from __future__ import annotations
 
 import math
+import os
 from typing import Optional
 
 import torch
@@ -57,6 +71,25 @@ def paged_cache_to_dense_rotated(kv_cache: Tensor, block_table: Tensor, seq_lens
     return mod.cda_fa2_paged_cache_to_dense_rotated(kv_cache, bt, sl, cb_K.contiguous(),
                                                     cb_V.contiguous(), int(block_size),
                                                     int(max_seq_len))
+
+
+_DENSE_MIN_QUERY_LEN = 256
+_DENSE_MAX_BYTES = 4 << 30
+
+
+def prefill_source(B: int, H_kv: int, max_query_len: int, max_seq_len: int) -> str:
+    """K/V source of the prefill kernel for this call: "dense" or
+    "compressed" (policy in the module docstring; host integers only, so the
+    choice never synchronises with the GPU)."""
+    mode = os.environ.get("CDA_PREFILL_SOURCE", "auto")
+    if mode in ("dense", "compressed"):
+        return mode
+    if mode != "auto":
+        raise ValueError(f"CDA_PREFILL_SOURCE must be auto, dense or compressed, not {mode!r}")
+    dense_bytes = 2 * B * max_seq_len * H_kv * 128 * 2
+    if max_query_len >= _DENSE_MIN_QUERY_LEN and dense_bytes <= _DENSE_MAX_BYTES:
+        return "dense"
+    return "compressed"
 
 
 def fa2_cda_prefill_varlen_v1(
@@ -108,7 +141,9 @@ def fa2_cda_prefill_varlen_v1(
     bt = block_table.to(torch.int32) if block_table.dtype != torch.int32 else block_table
     kv = kv_cache.view(-1, *kv_cache.shape[-2:]) if kv_cache.dim() == 4 else kv_cache
     out = output if output.is_contiguous() else torch.empty_like(output)
-    if return_dense_kv:
+    dense = return_dense_kv or prefill_source(B, kv.shape[-2], int(max_query_len),
+                                              int(max_seq_len)) == "dense"
+    if dense:
         k_rot, v_rot = paged_cache_to_dense_rotated(kv, bt, sl, cb_K=cb_K, cb_V=cb_V,
                                                     block_size=block_size,
                                                     max_seq_len=max_seq_len)

@@ -58,3 +58,23 @@ def test_choose_tile_n_policy():
     for B, N in ((1, 4096), (4, 65536), (32, 65536), (32, 1)):
         t = _choose_tile_n(N, B=B, H_q=32)
         assert t % 32 == 0 and t >= 32 and -(-N // t) <= 512
+
+
+def test_prefill_source_policy(monkeypatch):
+    """The prefill K/V source: the dense bridge for long query chunks whose
+    dense K/V fit in 4 GiB, compressed tiles otherwise; the environment
+    variable forces either and rejects other values."""
+    from sub0_amd.cda.kernels_cuda.fa2_cda import prefill_source
+    monkeypatch.delenv("CDA_PREFILL_SOURCE", raising=False)
+    assert prefill_source(8, 8, 7643, 7643) == "dense"
+    assert prefill_source(8, 8, 255, 7643) == "compressed"
+    assert prefill_source(32, 8, 64, 4096) == "compressed"
+    # 64 sequences x 65536 keys x 8 heads of fp16 K and V = 16 GiB: too large
+    assert prefill_source(64, 8, 4096, 65536) == "compressed"
+    monkeypatch.setenv("CDA_PREFILL_SOURCE", "compressed")
+    assert prefill_source(8, 8, 7643, 7643) == "compressed"
+    monkeypatch.setenv("CDA_PREFILL_SOURCE", "dense")
+    assert prefill_source(32, 8, 64, 4096) == "dense"
+    monkeypatch.setenv("CDA_PREFILL_SOURCE", "fast")
+    with pytest.raises(ValueError):
+        prefill_source(8, 8, 7643, 7643)

@@ -101,12 +101,14 @@ def test_decode_k2v2_fullsize_against_torch(gpu):
     assert err <= TOL
 
 
-def test_prefill_fullsize_against_torch(gpu):
+@pytest.mark.parametrize("source", ["compressed", "dense"])
+def test_prefill_fullsize_against_torch(gpu, source):
     import bench
     from sub0_amd import _native
-    print("[fullsize] prefill config 3 (8 sequences, 512-8192 tokens)", flush=True)
+    print(f"[fullsize] prefill config 3 (8 sequences, 512-8192 tokens) source={source}",
+          flush=True)
     w = bench.make_prefill_workload(gpu)
-    bench.prefill_call(w)()
+    bench.prefill_call(w, source)()
     torch.cuda.synchronize()
     out = w["out"]
     assert torch.isfinite(out).all()
