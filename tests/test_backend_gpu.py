@@ -20,13 +20,13 @@ H_Q, H_KV, D, BS = 32, 8, 128, 16
 class Scenario:
     """Three requests over one fp16-typed vLLM cache (nb, 16, 8, 72)."""
 
-    def __init__(self, dev, seed=77, fill=0x5A):
+    def __init__(self, dev, seed=77, fill=0x5A, nmax=160):
         from sub0_amd.cda.kernels_cuda.vllm_integration import cda_attn_v2 as A
         self.A = A
         self.dev = dev
         Impl = A.get_backend_classes()[1]
         self.impl = Impl(H_Q, D, 1.0 / np.sqrt(D), num_kv_heads=H_KV)
-        self.nmax = 160
+        self.nmax = nmax
         self.W = (self.nmax + BS - 1) // BS + 1
         self.B = 3
         self.bt = synth.permuted_block_table(seed, self.B, self.W)
@@ -152,3 +152,18 @@ def test_backend_decode_graph_replay(gpu):
         g.replay()
         torch.cuda.synchronize()
         assert torch.equal(o, eager)
+
+
+def test_backend_long_prefill_takes_dense_bridge(gpu, monkeypatch):
+    """A prefill step with a 300-token request (max_query_len >= 256: the
+    wrapper's default source is the dense bridge) and a follow-up decode."""
+    from sub0_amd.cda.kernels_cuda.fa2_cda import prefill_source
+    monkeypatch.delenv("CDA_PREFILL_SOURCE", raising=False)
+    assert prefill_source(3, H_KV, 300, 300) == "dense"
+    sc = Scenario(gpu, seed=79, nmax=320)
+    print("[backend] long prefill step lens=[300,5,260]", flush=True)
+    out, cache, Q, cu = sc.step([300, 5, 260])
+    check(out, sc.expected_prefill(cache, Q, cu, [0, 1, 2]))
+    print("[backend] decode after the long prefill", flush=True)
+    out, cache, Q, cu = sc.step([1, 1, 1])
+    check(out, sc.expected_decode(cache, Q, cu, [0, 1, 2]))
