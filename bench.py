@@ -235,6 +235,95 @@ def prefill_main(args) -> int:
     return 0
 
 
+# Reference Table 2 (RTX A6000, CUDA-graph medians, µs): CDA decode, FA2 fp16 on
+# uncompressed K/V, R2 dequant+FA2, R1 fused dequant+FA2
+# (results/table2_compute_path_iso/compute_path_isolation_cuda_graph.json:15-54).
+TABLE2_A6000 = {
+    (1, 4096): {"cda": 53.1, "fa_fp16": 43.0, "r2": 113.7, "r1": 170.0},
+    (1, 65536): {"cda": 297.0, "fa_fp16": 405.5, "r2": 1329.2, "r1": 1769.5},
+    (4, 65536): {"cda": 986.1, "r2": 5487.1, "r1": 6532.9},
+    (32, 16384): {"cda": 1936.9, "r2": 11852.8, "r1": 10401.8},
+}
+
+
+def table2_main(args) -> int:
+    """--table2: the reference's Table 2 cells on MI355X -- CDA decode against
+    the class-(a) comparators (R2: dense dequantised K/V + attention; R1:
+    compressed tiles dequantised on chip) and attention over uncompressed fp16
+    K/V; graph-replay medians.  One JSON line."""
+    import torch
+    import torch.nn.functional as F
+    from sub0_amd import _native
+    from sub0_amd.cda.kernels_cuda.class_a import dequant_fa2_decode, fused_dequant_fa2_decode
+
+    dev = torch.device("cuda:0")
+    scale = 1.0 / D ** 0.5
+    rows = []
+    for (B, N), pub in TABLE2_A6000.items():
+        w = make_workload(B, N, dev)
+        out2 = torch.empty_like(w["out"])
+        k_rot, v_rot = _native.paged_to_dense(w["cache"], w["bt"], w["seq"], w["cb"], w["cb"],
+                                              block_size=BS, max_seq_len=N)
+        kd = k_rot.view(B, N, H_KV, D).transpose(1, 2)
+        vd = v_rot.view(B, N, H_KV, D).transpose(1, 2)
+        q4 = w["q"].unsqueeze(2)
+        fns = {
+            "cda": decode_call(w),
+            "r2": lambda: dequant_fa2_decode(w["q"], w["cache"], w["bt"], w["seq"], out2,
+                                             cb_K=w["cb"], cb_V=w["cb"], rotation_fp32=w["R"],
+                                             block_size=BS, max_seq_len=N, scale=scale),
+            "r1": lambda: fused_dequant_fa2_decode(w["q"], w["cache"], w["bt"], w["seq"], out2,
+                                                   cb_K=w["cb"], cb_V=w["cb"], block_size=BS,
+                                                   scale=scale),
+            "fa_fp16": lambda: F.scaled_dot_product_attention(q4, kd, vd, scale=scale,
+                                                              enable_gqa=True),
+        }
+        row = {"B": B, "N": N}
+        for name, fn in fns.items():
+            try:
+                g = capture(fn, 3)
+                settle(g, 0.05)
+                row[f"{name}_us"] = round(replay_median_us(g, 20), 2)
+                del g
+            except Exception as e:   # not capturable: eager events
+                log(f"table2 {name} B={B} N={N}: eager timing ({e!r})")
+                torch.cuda.synchronize()
+                for _ in range(3):
+                    fn()
+                vals = []
+                for _ in range(20):
+                    a = torch.cuda.Event(enable_timing=True)
+                    b = torch.cuda.Event(enable_timing=True)
+                    a.record()
+                    fn()
+                    b.record()
+                    torch.cuda.synchronize()
+                    vals.append(a.elapsed_time(b) * 1000.0)
+                row[f"{name}_us"] = round(statistics.median(vals), 2)
+                row[f"{name}_eager"] = True
+        for name in ("r2", "r1", "fa_fp16"):
+            row[f"{name}_over_cda"] = round(row[f"{name}_us"] / row["cda_us"], 2)
+            if name in pub:
+                row[f"a6000_{name}_over_cda"] = round(pub[name] / pub["cda"], 2)
+        # The ideal fp16 attention: its K/V bytes (B*N*8*256*2) at 8 TB/s.
+        row["fa_fp16_hbm_floor_us"] = round(B * N * H_KV * D * 2 * 2 / (PEAK_GBS * 1e3), 2)
+        row["a6000_cda_us"] = pub["cda"]
+        row["cda_speedup_vs_a6000"] = round(pub["cda"] / row["cda_us"], 2)
+        log(json.dumps(row))
+        rows.append(row)
+        del w, k_rot, v_rot, kd, vd, out2, fns
+        torch.cuda.empty_cache()
+    line = {"metric": "decode latency, CDA vs class-(a) comparators (reference Table 2 cells)",
+            "unit": "us", "n_gpus": 1, "higher_is_better": False, "data": "synthetic",
+            "config": {"workload": "K4V4 paged decode, 32 Q / 8 KV heads, d=128, block 16"},
+            "notes": "fa_fp16 and the attention of r2 are torch scaled_dot_product_attention "
+                     "(ROCm), which does not split the keys of a one-query decode; "
+                     "fa_fp16_hbm_floor_us is the fp16 K/V bytes at 8 TB/s",
+            "rows": rows}
+    print(json.dumps(line), flush=True)
+    return 0
+
+
 def make_encode_workload(dev, levels: int, seed: int = 0xCDA2, n_seq: int = 64,
                          max_new: int = 256, ctx: int = 4096):
     """n_seq sequences each appending U[1, max_new] new
@@ -746,6 +835,9 @@ def main(argv=None):
     ap.add_argument("--e2e-batch", type=int, default=32)
     ap.add_argument("--e2e-prefix", type=int, default=16384)
     ap.add_argument("--e2e-steps", type=int, default=256)
+    ap.add_argument("--table2", action="store_true",
+                    help="the reference's Table 2 cells: CDA decode vs the class-(a) "
+                         "comparators and fp16 attention")
     ap.add_argument("--k2v2", action="store_true",
                     help="decode over a K2V2 cache (4-level codebook, 80-byte slots) instead of K4V4")
     ap.add_argument("--general-kernel", action="store_true",
@@ -781,6 +873,8 @@ def main(argv=None):
         return encode_main(args)
     if args.e2e:
         return e2e_main(args)
+    if args.table2:
+        return table2_main(args)
     if args.general_kernel:
         _native.set_stream_kernel(False)
     B, N = args.B, args.N

@@ -633,6 +633,28 @@ def _build_backend_classes():
                            group_size=self.group_size, block_size=block_size,
                            scale=self.scale, max_seq_len=attn_metadata.max_seq_len)
 
+        def _call_dequant_fa2_decode(self, q_in, kv_cache_flat, attn_metadata, out_buf, *,
+                                     cb_K, cb_V, rotation_fp32, rotation_fp16, block_size):
+            """Class-(a) R2 comparator (``cda_attn_v2.py:1062-1184``): dense
+            dequantised K/V, then attention over them."""
+            from sub0_amd.cda.kernels_cuda.class_a import dequant_fa2_decode
+            B = q_in.shape[0]
+            dequant_fa2_decode(q_in, kv_cache_flat, attn_metadata.block_table[:B],
+                               attn_metadata.seq_lens[:B], out_buf, cb_K=cb_K, cb_V=cb_V,
+                               rotation_fp32=rotation_fp32, block_size=block_size,
+                               max_seq_len=attn_metadata.max_seq_len, scale=self.scale)
+
+        def _call_fused_dequant_fa2_decode(self, q_in, kv_cache_flat, attn_metadata, out_buf, *,
+                                           cb_K, cb_V, rotation_fp32, rotation_fp16,
+                                           block_size):
+            """Class-(a) R1 comparator (``cda_attn_v2.py:1186-1250``): tiles of
+            the compressed cache dequantised on chip inside the attention."""
+            from sub0_amd.cda.kernels_cuda.class_a import fused_dequant_fa2_decode
+            B = q_in.shape[0]
+            fused_dequant_fa2_decode(q_in, kv_cache_flat, attn_metadata.block_table[:B],
+                                     attn_metadata.seq_lens[:B], out_buf, cb_K=cb_K,
+                                     cb_V=cb_V, block_size=block_size, scale=self.scale)
+
         def _forward_decode(self, query, kv_cache, output, attn_metadata):
             """One query token per request over the paged cache, written
             straight into ``output`` when it is an fp16 (T, H_q, D) or
@@ -641,10 +663,10 @@ def _build_backend_classes():
             if kv_cache.shape[3] % 16 != 0:
                 raise NotImplementedError(
                     "CDA decode requires 16-byte aligned compressed slots.")
-            if _DECODE_BACKEND != "hmma_v1":
+            if _DECODE_BACKEND not in ("hmma_v1", "dequant_fa2", "fused_dequant_fa2"):
                 raise NotImplementedError(
-                    f"CDA_DECODE_BACKEND={_DECODE_BACKEND!r} (the dequantise + FlashAttention "
-                    "comparators) is not available in the MI355X build.")
+                    f"CDA_DECODE_BACKEND={_DECODE_BACKEND!r} is not a decode route; expected "
+                    "hmma_v1, dequant_fa2 or fused_dequant_fa2.")
             cb_K, cb_V, r32, r16, flat, bs = _time_call(
                 "decode_setup", lambda: self._setup(query, kv_cache))
             q = query.squeeze(2) if query.dim() == 4 else query
@@ -656,9 +678,18 @@ def _build_backend_classes():
             direct = out is not None and output.shape[0] == T
             if not direct:
                 out = torch.empty_like(q)
-            _time_call("decode_hmma", lambda: self._call_decode_hmma_v1(
-                q, flat, attn_metadata, out, cb_K=cb_K, cb_V=cb_V, rotation_fp32=r32,
-                rotation_fp16=r16, block_size=bs))
+            if _DECODE_BACKEND == "dequant_fa2":
+                _time_call("decode_dequant_fa2", lambda: self._call_dequant_fa2_decode(
+                    q, flat, attn_metadata, out, cb_K=cb_K, cb_V=cb_V, rotation_fp32=r32,
+                    rotation_fp16=r16, block_size=bs))
+            elif _DECODE_BACKEND == "fused_dequant_fa2":
+                _time_call("decode_fused_dequant_fa2", lambda: self._call_fused_dequant_fa2_decode(
+                    q, flat, attn_metadata, out, cb_K=cb_K, cb_V=cb_V, rotation_fp32=r32,
+                    rotation_fp16=r16, block_size=bs))
+            else:
+                _time_call("decode_hmma", lambda: self._call_decode_hmma_v1(
+                    q, flat, attn_metadata, out, cb_K=cb_K, cb_V=cb_V, rotation_fp32=r32,
+                    rotation_fp16=r16, block_size=bs))
             if not direct:
                 _time_call("decode_output_copy", lambda: _copy_out(output, out, T))
             return output
