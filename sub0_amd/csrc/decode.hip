@@ -977,15 +977,23 @@ __device__ __forceinline__ float wave_sum(float v) {
 // row reads (lane j reads row j) fall in distinct banks.
 constexpr int kRPad = kD + 4;
 
+// HPB heads per 256-thread block: 4 (one wave per head) when the grid fills
+// the chip, else 1 (the four waves take interleaved 32-split batches of one
+// head and their partial sums are added in a fixed order).
+template <int HPB>
 __global__ void __launch_bounds__(256)
 combine_kernel(const float *part_o, const float *part_ml, const float *R, uint16_t *out,
                int H_q, int n_splits) {
+    static_assert(HPB == 4 || HPB == 1, "heads per block");
+    constexpr int kWph = 4 / HPB;                  // waves per head
     __shared__ __align__(16) float Rs[kD * kRPad];
-    __shared__ float wts[kHeadsPerBlock][kMaxSplits];
-    __shared__ __align__(16) float orot[kHeadsPerBlock][kD];
+    __shared__ float wts[4][kMaxSplits];
+    __shared__ __align__(16) float orot[4][kD];
     const int b = blockIdx.y, t = threadIdx.x;
-    const int h0 = blockIdx.x * kHeadsPerBlock;
-    const int hh = t >> 6, lane = t & 63;
+    const int h0 = blockIdx.x * HPB;
+    const int hh = (HPB == 4) ? (t >> 6) : 0, lane = t & 63;
+    const int wsub = (HPB == 4) ? 0 : (t >> 6);   // this wave's share of the splits
+    const int wslot = t >> 6;                      // this wave's rows of wts / orot
     const int h = h0 + hh;
     float4 rr[kD * kD / 4 / 256];
     {
@@ -1016,7 +1024,7 @@ combine_kernel(const float *part_o, const float *part_ml, const float *R, uint16
         for (int i = 0; i < kPer; ++i) {
             const int s = lane + 64 * i;
             const float w = (ml[i].x == -INFINITY) ? 0.0f : exp2f(ml[i].x - mx);
-            if (s < n_splits) wts[hh][s] = w;
+            if (s < n_splits) wts[wslot][s] = w;
             if (w != 0.0f) lp += w * ml[i].y;
         }
         L = wave_sum(lp);
@@ -1035,7 +1043,7 @@ combine_kernel(const float *part_o, const float *part_ml, const float *R, uint16
         const float *po = part_o + base * kD + d4;
         const int64_t step = (int64_t)H_q * kD;
         float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
-        for (int s0 = 0; s0 < n_splits; s0 += 32) {
+        for (int s0 = 32 * wsub; s0 < n_splits; s0 += 32 * kWph) {
             float4 v[16];
 #pragma unroll
             for (int u = 0; u < 16; ++u) {
@@ -1046,7 +1054,7 @@ combine_kernel(const float *part_o, const float *part_ml, const float *R, uint16
 #pragma unroll
             for (int u = 0; u < 16; ++u) {
                 const int s = s0 + 2 * u + half;
-                const float w = (s < n_splits) ? wts[hh][s] : 0.0f;
+                const float w = (s < n_splits) ? wts[wslot][s] : 0.0f;
                 o.x = fmaf(w, v[u].x, o.x);
                 o.y = fmaf(w, v[u].y, o.y);
                 o.z = fmaf(w, v[u].z, o.z);
@@ -1063,15 +1071,30 @@ combine_kernel(const float *part_o, const float *part_ml, const float *R, uint16
         o.z = sum_halves(o.z);
         o.w = sum_halves(o.w);
         const float inv = 1.0f / fmaxf(L, 1e-30f);
-        if (half == 0) {
+        if (HPB == 4 && half == 0) {
             orot[hh][d4 + 0] = h2f(__half_as_ushort(__float2half_rn(o.x * inv)));
             orot[hh][d4 + 1] = h2f(__half_as_ushort(__float2half_rn(o.y * inv)));
             orot[hh][d4 + 2] = h2f(__half_as_ushort(__float2half_rn(o.z * inv)));
             orot[hh][d4 + 3] = h2f(__half_as_ushort(__float2half_rn(o.w * inv)));
         }
+        if (HPB == 1 && half == 0)
+            *reinterpret_cast<float4 *>(&orot[wsub][d4]) = make_float4(o.x, o.y, o.z, o.w);
     }
     __syncthreads();
-    if (!live) return;
+    if (!live || wsub != 0) return;
+    if (HPB == 1) {
+        // Wave 0: add the four waves' partial sums (fixed order), normalise,
+        // round O_rot to fp16.
+        const float inv = 1.0f / fmaxf(L, 1e-30f);
+        const float s0 = ((orot[0][lane] + orot[1][lane]) + orot[2][lane]) + orot[3][lane];
+        const float s1 = ((orot[0][lane + 64] + orot[1][lane + 64]) + orot[2][lane + 64]) +
+                         orot[3][lane + 64];
+        // Every lane has read all four rows before row 0 is overwritten.
+        __builtin_amdgcn_wave_barrier();
+        orot[0][lane] = h2f(__half_as_ushort(__float2half_rn(s0 * inv)));
+        orot[0][lane + 64] = h2f(__half_as_ushort(__float2half_rn(s1 * inv)));
+        __builtin_amdgcn_wave_barrier();
+    }
     const float *r0 = Rs + lane * kRPad;
     const float *r1 = Rs + (lane + 64) * kRPad;
     float a0 = 0.0f, a1 = 0.0f;
@@ -1280,8 +1303,13 @@ extern "C" int cda_decode_full_hmma_v3(const void *q, const void *kv_cache, int6
     if (g_split_stop && hipEventRecord(g_split_stop, st) != hipSuccess)
         return fail(CDA_E_HIP, "cda_decode_full_hmma_v3: hipEventRecord(stop) failed");
 
-    combine_kernel<<<head_grid, 256, 0, st>>>(p.part_o, p.part_ml, rot_f32,
-                                                 static_cast<uint16_t *>(out), H_q, ns);
+    // One head per block when four per block would leave CUs idle.
+    if ((int64_t)head_grid.x * B < num_cus())
+        combine_kernel<1><<<dim3(H_q, B), 256, 0, st>>>(p.part_o, p.part_ml, rot_f32,
+                                                        static_cast<uint16_t *>(out), H_q, ns);
+    else
+        combine_kernel<4><<<head_grid, 256, 0, st>>>(p.part_o, p.part_ml, rot_f32,
+                                                     static_cast<uint16_t *>(out), H_q, ns);
     CDA_LAUNCH_CHECK("combine_kernel");
     return CDA_OK;
 }
