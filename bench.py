@@ -838,6 +838,8 @@ def main(argv=None):
     ap.add_argument("--table2", action="store_true",
                     help="the reference's Table 2 cells: CDA decode vs the class-(a) "
                          "comparators and fp16 attention")
+    ap.add_argument("--gs8", action="store_true",
+                    help="GQA group of 8 (64 Q / 8 KV heads, the 70B shape) instead of 4")
     ap.add_argument("--k2v2", action="store_true",
                     help="decode over a K2V2 cache (4-level codebook, 80-byte slots) instead of K4V4")
     ap.add_argument("--general-kernel", action="store_true",
@@ -879,6 +881,9 @@ def main(argv=None):
         _native.set_stream_kernel(False)
     B, N = args.B, args.N
 
+    global H_Q
+    if args.gs8:
+        H_Q = 8 * H_KV
     levels = 4 if args.k2v2 else 16
     w = make_workload(B, N, dev, identity_bt=args.identity_block_table, levels=levels)
     fn = decode_call(w, args.tile_n)
@@ -896,7 +901,7 @@ def main(argv=None):
     med_us = replay_median_us(g, 20)
     k_us = split_kernel_us(fn, max(5, args.steps))
     slot_data = 136 if levels == 16 else 72
-    nbytes = _native.decode_algorithmic_bytes(B, N, slot_data=slot_data)
+    nbytes = _native.decode_algorithmic_bytes(B, N, H_q=H_Q, slot_data=slot_data)
     value = nbytes / (ms_per_step * 1e-3) / 1e9
     achieved = nbytes / (k_us * 1e-6) / 1e9
     tile, splits = _native.decode_plan(B, H_Q, H_KV, N, args.tile_n)
@@ -930,7 +935,8 @@ def main(argv=None):
             Path(args.sweep_out).write_text(json.dumps(sweep, indent=1) + "\n")
 
     cpu = None
-    if not args.no_cpu_baseline and levels == 16:   # the CPU baseline is the K4V4 config 0
+    # the CPU baseline is config 0 (K4V4, 32 Q heads)
+    if not args.no_cpu_baseline and levels == 16 and not args.gs8:
         try:
             cpu = cpu_baseline()
         except Exception as e:  # the baseline is reported, never required
@@ -941,7 +947,7 @@ def main(argv=None):
     # Both code widths (8 KV heads, one codebook) take the page-streaming kernel
     # unless it is switched off.
     kernel = "decode_split_kernel" if args.general_kernel else "decode_stream_kernel"
-    traffic = load_traffic(kernel, B, N) if levels == 16 else None
+    traffic = load_traffic(kernel, B, N) if levels == 16 and not args.gs8 else None
     variant = "K4V4" if levels == 16 else "K2V2"
     line = {
         "metric": METRIC,
@@ -960,8 +966,10 @@ def main(argv=None):
         "dtype": f"u{2 if levels == 4 else 4} codes, fp16 MFMA operands, fp32 accumulate",
         "data": "synthetic (K,V,q ~ N(0,1) fp16, K with 4 outlier channels x8, "
                 f"Lloyd-beta {levels}-level codebook, permuted block table)",
-        "config": {"workload": f"{variant} paged decode, B={B}, N={N}, Llama-3-8B heads "
-                               "(32 Q / 8 KV, d=128), block 16",
+        "config": {"workload": f"{variant} paged decode, B={B}, N={N}, "
+                               + ("70B-shaped heads (64 Q / 8 KV" if args.gs8
+                                  else "Llama-3-8B heads (32 Q / 8 KV")
+                               + ", d=128), block 16",
                    "B": B, "N": N, "H_q": H_Q, "H_kv": H_KV, "head_dim": D, "block_size": BS,
                    "tile_n": tile, "splits": splits, "algorithmic_bytes": nbytes},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_GBS,
