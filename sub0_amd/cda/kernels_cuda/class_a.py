@@ -43,7 +43,10 @@ def dequant_fa2_decode(q: Tensor, kv_cache: Tensor, block_table: Tensor, seq_len
     q_rot = _hadamard_or_matmul(q.contiguous(), rotation_fp32)
     k = k_rot.view(B, N, H_kv, D).transpose(1, 2)
     v = v_rot.view(B, N, H_kv, D).transpose(1, 2)
-    mask = (torch.arange(N, device=q.device)[None, :] < seq_lens[:, None].to(torch.int64))
+    # An empty sequence keeps key 0 visible: its dense row is zero, so the
+    # output is zero (as the CDA decode writes) rather than a 0/0.
+    n_vis = seq_lens.to(torch.int64).clamp(min=1)
+    mask = torch.arange(N, device=q.device)[None, :] < n_vis[:, None]
     o_rot = F.scaled_dot_product_attention(q_rot.unsqueeze(2), k, v,
                                            attn_mask=mask[:, None, None, :], scale=scale,
                                            enable_gqa=H_q != H_kv)

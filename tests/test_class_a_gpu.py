@@ -19,7 +19,8 @@ def _check(out, exp):
 
 
 @pytest.mark.parametrize("route", ["dequant_fa2", "fused_dequant_fa2"])
-@pytest.mark.parametrize("gs,seq_lens", [(4, [300, 1, 77, 1031]), (8, [500, 1200])])
+@pytest.mark.parametrize("gs,seq_lens", [(4, [300, 1, 77, 1031]), (8, [500, 1200]),
+                                         (4, [0, 65, 16])])
 def test_comparator_matches_checker(gpu, route, gs, seq_lens):
     from sub0_amd.cda.kernels_cuda import class_a
     print(f"[class-a] route={route} gs={gs} seq_lens={seq_lens}", flush=True)
@@ -31,8 +32,8 @@ def test_comparator_matches_checker(gpu, route, gs, seq_lens):
     scale = 1.0 / np.sqrt(128)
     if route == "dequant_fa2":
         class_a.dequant_fa2_decode(q, cache, bt, sl, out, cb_K=cb, cb_V=cb, rotation_fp32=R,
-                                   block_size=case.block_size, max_seq_len=int(max(seq_lens)),
-                                   scale=scale)
+                                   block_size=case.block_size,
+                                   max_seq_len=max(1, int(max(seq_lens))), scale=scale)
     else:
         class_a.fused_dequant_fa2_decode(q, cache, bt, sl, out, cb_K=cb, cb_V=cb,
                                          block_size=case.block_size, scale=scale)
