@@ -251,7 +251,9 @@ def prefill_main(args) -> int:
                                "d=128, K4V4 paged cache (block 16, permuted)",
                    "lengths": w["lens"], "tokens": w["T"], "flops": w["flops"]},
         "roofline": {"bound": "mfma", "achieved": round(k_tflops, 1), "peak": peak,
-                     "unit": "TFLOP/s", "frac": round(k_tflops / peak, 4), "traffic": None,
+                     "unit": "TFLOP/s", "frac": round(k_tflops / peak, 4),
+                     "traffic": load_kernel_traffic("prefill_kernel<dense>" if chosen == "dense"
+                                                    else "prefill_kernel<paged>", "config3"),
                      "kernel": "prefill_kernel<dense>" if chosen == "dense"
                      else "prefill_kernel<paged>", "kernel_ms": round(kernel_ms, 4)},
         "prefill_source": chosen,
@@ -465,7 +467,8 @@ def encode_main(args) -> int:
                                "K4V4 (144-byte slots), permuted block table",
                    "tokens": w["T"], "algorithmic_bytes": w["bytes"]},
         "roofline": {"bound": "hbm", "achieved": round(k_gbs, 1), "peak": 8000.0, "unit": "GB/s",
-                     "frac": round(k_gbs / 8000.0, 4), "traffic": None,
+                     "frac": round(k_gbs / 8000.0, 4),
+                     "traffic": load_kernel_traffic("paged_encode_kernel<16>", "config2"),
                      "kernel": "paged_encode_kernel<16>", "kernel_us": round(k_us, 2)},
         "k2v2": {"tokens": w2["T"], "algorithmic_bytes": w2["bytes"], "ms_per_step": round(ms2, 5),
                  "value": round(w2["bytes"] / (ms2 * 1e-3) / 1e9, 1),
@@ -832,6 +835,19 @@ def cpu_baseline(threads: int | None = None, reps: int = 3):
 
 
 # -------------------------------------------------------------------- main --
+
+def load_kernel_traffic(kernel, workload):
+    """HBM bytes per launch of `kernel` on a named workload (config2, config3)
+    from the committed rocprofv3 PMC summary, or None."""
+    p = ROOT / "profiles" / "kernel_traffic.json"
+    if not p.is_file():
+        return None
+    try:
+        cell = json.loads(p.read_text()).get("kernels", {}).get(kernel, {}).get(workload)
+        return None if cell is None else int(cell["hbm_bytes_per_launch"])
+    except (ValueError, KeyError, TypeError):
+        return None
+
 
 def load_traffic(kernel, B, N):
     """HBM bytes per launch of `kernel` from the committed rocprofv3 PMC summary."""
