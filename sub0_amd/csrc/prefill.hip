@@ -40,6 +40,7 @@ constexpr int kD = 128;
 constexpr int kBN = 64;                  // keys per tile
 constexpr int kWaves = 8;
 constexpr int kThreads = 64 * kWaves;
+constexpr uint32_t kXcds = 8;            // MI355X: 8 XCDs, each with its own L2
 constexpr float kLog2e = 1.4426950408889634f;
 
 // LDS: two tile buffers, then the code-byte dequant tables (paged source),
@@ -314,8 +315,25 @@ prefill_kernel(PrefillParams p) {
     __shared__ __align__(16) uint8_t smem[kPrefillLds];
     constexpr int QB = 32 * (kWaves / GS);          // queries per workgroup
 
-    const int b = blockIdx.y;
-    const int h = blockIdx.z;
+    // XCD-aware order: workgroups are dealt to the 8 XCDs round-robin by
+    // linear id, so XCD k is given the k-th contiguous eighth of the logical
+    // order (query blocks of one (sequence, KV head) adjacent, longest first).
+    // Workgroups reading the same keys then share one XCD's L2.
+    uint32_t lx, ly, lz;
+    {
+        const uint32_t gx = gridDim.x, gy = gridDim.y;
+        const uint32_t n = gx * gy * gridDim.z;
+        const uint32_t pid = blockIdx.x + gx * (blockIdx.y + gy * blockIdx.z);
+        const uint32_t xcd = pid % kXcds, slot = pid / kXcds;
+        const uint32_t per = n / kXcds, rem = n % kXcds;
+        const uint32_t lid = xcd < rem ? xcd * (per + 1) + slot
+                                       : rem * (per + 1) + (xcd - rem) * per + slot;
+        lx = lid % gx;
+        ly = (lid / gx) % gy;
+        lz = lid / (gx * gy);
+    }
+    const int b = (int)ly;
+    const int h = (int)lz;
     const int tid = threadIdx.x;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int lane = tid & 63;
@@ -329,7 +347,7 @@ prefill_kernel(PrefillParams p) {
     // Consecutive workgroups share one (sequence, KV head) and so read the
     // same keys: ordering the grid by causal work across sequences instead
     // was measured 30-40 % slower (the L2 working set grows).
-    const int q0 = (gridDim.x - 1 - blockIdx.x) * QB;
+    const int q0 = (int)(gridDim.x - 1 - lx) * QB;
     if (q0 >= seq_q) return;
     const int off = seq_k - seq_q;                   // bottom-right causal alignment
     const int q_last = min(q0 + QB, seq_q) - 1;
