@@ -8,9 +8,10 @@
 //
 // A 16-lane row of a wave encodes one 128-vector: lane j holds elements
 // 8j..8j+7 (one 16-byte load), so the first three butterfly stages and the
-// first three levels of the norm tree stay in registers and four stages cross
-// lanes (DPP within the row); a wave encodes four vectors of one role (K or
-// V).  The butterfly runs in float64, where every partial sum of fp16 inputs
+// first three levels of the norm tree stay in registers; an LDS transpose
+// turns three of the other four butterfly stages into register stages, one
+// crosses lanes (DPP within the row), as do four levels of the norm tree; a
+// wave encodes four vectors of one role (K or V).  The butterfly runs in float64, where every partial sum of fp16 inputs
 // is exact, so the rotated value is rounded once, to fp16, exactly as the
 // reference rounds its fp32 matmul result back to the input dtype.  The
 // squared norm is summed in float64 in a fixed pairwise-tree order (element
@@ -112,6 +113,7 @@ paged_encode_kernel(EncodeParams p) {
     constexpr int KB = kD * (L == 16 ? 4 : 2) / 8;   // code bytes per role
     __shared__ float4 tri[2][L / 2];
     __shared__ float cbl[2][L];
+    __shared__ double xt[4 * kEncWaves][kD];      // one 128-vector per 16-lane row
     if (threadIdx.x < L) {
         const int r = threadIdx.x / (L / 2), i = threadIdx.x % (L / 2);
         const float *c = r ? p.cb_v : p.cb_k;
@@ -147,21 +149,45 @@ paged_encode_kernel(EncodeParams p) {
             x[2 * i + 1] = (double)h2f((uint16_t)(ws[i] >> 16));
         }
     }
-    // Sylvester butterflies: element bits 0-2 in registers, bits 3-6 across
-    // lanes j ^ 1, 2, 4, 8 (exact in float64).
+    // Sylvester butterflies, exact in float64 (so their order is free):
+    // element bits 0-2 in registers; then a transpose through LDS gives lane
+    // j the elements (j & 7) + 8 r + 64 (j >> 3), r = 0..7, so bits 3-5 are
+    // register stages too and only bit 6 crosses lanes (j ^ 8); a second
+    // transpose restores elements 8j..8j+7 to lane j.
+    auto bfly_regs = [&]() CDA_INLINE {
 #pragma unroll
-    for (int m = 1; m < 8; m <<= 1)
+        for (int m = 1; m < 8; m <<= 1)
 #pragma unroll
-        for (int i = 0; i < 8; ++i)
-            if (!(i & m)) {
-                const double a = x[i], b = x[i | m];
-                x[i] = a + b;
-                x[i | m] = a - b;
-            }
-    bfly_lanes<1>(x, lane);
-    bfly_lanes<2>(x, lane);
-    bfly_lanes<4>(x, lane);
-    bfly_lanes<8>(x, lane);
+            for (int i = 0; i < 8; ++i)
+                if (!(i & m)) {
+                    const double a = x[i], b = x[i | m];
+                    x[i] = a + b;
+                    x[i | m] = a - b;
+                }
+    };
+    bfly_regs();
+    {
+        double *row = xt[threadIdx.x >> 4];       // this lane's vector (128 doubles)
+        const int e0 = (j & 7) + 64 * (j >> 3);
+        double2 *mine = reinterpret_cast<double2 *>(row + 8 * j);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) mine[i] = make_double2(x[2 * i], x[2 * i + 1]);
+        __builtin_amdgcn_wave_barrier();
+#pragma unroll
+        for (int r = 0; r < 8; ++r) x[r] = row[e0 + 8 * r];
+        bfly_regs();
+        bfly_lanes<8>(x, lane);
+        __builtin_amdgcn_wave_barrier();
+#pragma unroll
+        for (int r = 0; r < 8; ++r) row[e0 + 8 * r] = x[r];
+        __builtin_amdgcn_wave_barrier();
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const double2 v = mine[i];
+            x[2 * i] = v.x;
+            x[2 * i + 1] = v.y;
+        }
+    }
     const double hsc = (double)__int_as_float(0x3db504f3);   // fp32(1/sqrt(128))
     float f[8];
 #pragma unroll
