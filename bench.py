@@ -270,6 +270,67 @@ def prefill_main(args) -> int:
     return 0
 
 
+def prefill_chunk_main(args) -> int:
+    """--prefill-chunk: chunked prefill, Q new queries per sequence over K keys
+    (the last Q keys are the chunk's own, causal).  Times the compressed-tile
+    kernel with its key split (the default for such chunks), without it, and
+    the dense bridge; one JSON line (not the headline metric)."""
+    import torch
+    from sub0_amd import _native
+    dev = torch.device("cuda:0")
+    B, Qn, K = args.chunk_b, args.chunk_q, args.chunk_k
+    w = make_prefill_workload(dev, n_seq=B, lo=K, hi=K)
+    gpu = torch.Generator(device=dev).manual_seed(0xC0DE)
+    q = torch.randn(B * Qn, H_Q, D, generator=gpu, device=dev, dtype=torch.float16)
+    cu = torch.arange(0, B + 1, dtype=torch.int32, device=dev) * Qn
+    out = torch.empty_like(q)
+    flops = B * 4 * H_Q * D * (Qn * (K - Qn) + Qn * (Qn + 1) // 2)
+    ws = torch.empty(_native.prefill_workspace_size(B, B * Qn, H_Q, H_KV, Qn, K) + 256,
+                     dtype=torch.uint8, device=dev)
+    k_rot, v_rot = _native.paged_to_dense(w["cache"], w["bt"], w["seq"], w["cb"], w["cb"],
+                                          block_size=BS, max_seq_len=K)
+    cu_k = torch.arange(0, B + 1, dtype=torch.int32, device=dev) * K
+    sc = 1.0 / D ** 0.5
+    variants = {
+        "split": lambda: _native.prefill_paged(q, w["cache"], w["bt"], cu, w["seq"], w["cb"],
+                                               w["cb"], out, block_size=BS, max_query_len=Qn,
+                                               scale=sc, max_seq_len=K, workspace=ws),
+        "unsplit": lambda: _native.prefill_paged(q, w["cache"], w["bt"], cu, w["seq"], w["cb"],
+                                                 w["cb"], out, block_size=BS, max_query_len=Qn,
+                                                 scale=sc),
+        "dense_kernel": lambda: _native.fa2_varlen_fwd_hadamard(q, k_rot, v_rot, out, cu, cu_k,
+                                                                w["seq"], Qn, K, sc),
+    }
+    res = {}
+    outs = {}
+    for name, fn in variants.items():
+        g = capture(fn, args.warmup)
+        settle(g)
+        res[name] = replay_median_us(g, max(20, args.steps))
+        torch.cuda.synchronize()
+        outs[name] = out.clone()
+        del g
+    err = float((outs["split"].float() - outs["unsplit"].float()).abs().max())
+    us = res["split"]
+    peak = 2500.0
+    tf = flops / (us * 1e-6) / 1e12
+    line = {
+        "metric": "chunked prefill us/call from the K4V4 cache (key split)",
+        "value": round(us, 2), "unit": "us", "n_gpus": 1, "steps": max(20, args.steps),
+        "warmup": args.warmup, "higher_is_better": False,
+        "dtype": "fp16 MFMA operands, fp32 accumulate", "data": "synthetic",
+        "config": {"workload": f"{B} x {Qn} queries over {K} keys, causal, 32 Q / 8 KV heads, "
+                               "d=128, K4V4 paged cache (block 16, permuted)",
+                   "B": B, "queries": Qn, "keys": K, "flops": flops},
+        "roofline": {"bound": "mfma", "achieved": round(tf, 2), "peak": peak, "unit": "TFLOP/s",
+                     "frac": round(tf / peak, 5)},
+        "unsplit_us": round(res["unsplit"], 2), "dense_kernel_us": round(res["dense_kernel"], 2),
+        "split_vs_unsplit_max_abs": err,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
 # Reference Table 2 (RTX A6000, CUDA-graph medians, µs): CDA decode, FA2 fp16 on
 # uncompressed K/V, R2 dequant+FA2, R1 fused dequant+FA2
 # (results/table2_compute_path_iso/compute_path_isolation_cuda_graph.json:15-54).
@@ -881,6 +942,11 @@ def main(argv=None):
     ap.add_argument("--e2e", action="store_true",
                     help="BASELINE config 4: decode loop of a Mistral-shaped model through the "
                          "cda_v2 backend (one JSON line)")
+    ap.add_argument("--prefill-chunk", action="store_true",
+                    help="chunked prefill (--chunk-b x --chunk-q queries over --chunk-k keys)")
+    ap.add_argument("--chunk-b", type=int, default=1)
+    ap.add_argument("--chunk-q", type=int, default=16)
+    ap.add_argument("--chunk-k", type=int, default=16384)
     ap.add_argument("--e2e-batch", type=int, default=32)
     ap.add_argument("--e2e-prefix", type=int, default=16384)
     ap.add_argument("--e2e-steps", type=int, default=256)
@@ -920,6 +986,8 @@ def main(argv=None):
     _native.lib()
     if args.prefill:
         return prefill_main(args)
+    if args.prefill_chunk:
+        return prefill_chunk_main(args)
     if args.encode:
         return encode_main(args)
     if args.e2e:

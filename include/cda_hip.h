@@ -134,6 +134,31 @@ int cda_prefill_paged_hadamard(const void *q, const void *kv_cache, int64_t num_
                                const float *cb_v, int levels, void *out, int T, int H_q,
                                int block_size, int max_query_len, float scale, void *stream);
 
+/* Same operation as cda_prefill_paged_hadamard, for short query chunks over
+ * long contexts: when the query blocks x sequences x KV heads leave most CUs
+ * idle (fewer than 256 workgroups), the keys of each query block are split
+ * (at least 256 keys per split, at most 64 splits); the splits write
+ * unnormalised partials (O, m, l) into the workspace and a combine kernel
+ * merges them (attention.py:239-272) before the fp16 rounding of O_rot and
+ * the inverse rotation.  When no split pays it runs the unsplit kernel and
+ * ignores the workspace.  Same reference call site as above
+ * (fa2_cda.py:98-230; the reference has no split form).
+ *   max_seq_len:   upper bound of seq_lens[b] (the longest key range).
+ *   workspace:     device scratch, 256-byte aligned, of at least
+ *                  cda_prefill_workspace_size(B, T, H_q, H_kv, max_query_len,
+ *                  max_seq_len) bytes (0: no split, workspace may be NULL).
+ * Calls sharing one workspace must not overlap.
+ */
+size_t cda_prefill_workspace_size(int B, int T, int H_q, int H_kv, int max_query_len,
+                                  int max_seq_len);
+int cda_prefill_paged_hadamard_ws(const void *q, const void *kv_cache, int64_t num_slots,
+                                  int slot_bytes, int H_kv, const int32_t *block_table,
+                                  int bt_stride, const int32_t *cu_seqlens_q,
+                                  const int32_t *seq_lens, int B, const float *cb_k,
+                                  const float *cb_v, int levels, void *out, int T, int H_q,
+                                  int block_size, int max_query_len, int max_seq_len, float scale,
+                                  void *workspace, size_t workspace_bytes, void *stream);
+
 /* Replaces the reference pybind function
  *   cda_fa2_varlen_fwd_hadamard(Q, k_rot, v_rot, out, cu_q, cu_k, seqused_k,
  *                               max_q, max_k, scale)      (causal only)

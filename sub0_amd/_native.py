@@ -31,6 +31,8 @@ SYMBOLS = (
     "cda_decode_set_stream_kernel",
     "cda_paged_encode_fused",
     "cda_prefill_paged_hadamard",
+    "cda_prefill_workspace_size",
+    "cda_prefill_paged_hadamard_ws",
     "cda_fa2_varlen_fwd_hadamard",
     "cda_fa2_paged_cache_to_dense_rotated",
     "cda_hadamard128_fp16",
@@ -92,6 +94,12 @@ def lib():
         L.cda_prefill_paged_hadamard.argtypes = [
             _P, _P, _I64, _I32, _I32, _P, _I32, _P, _P, _I32, _P, _P, _I32, _P, _I32, _I32,
             _I32, _I32, _F32, _P]
+        L.cda_prefill_workspace_size.restype = _SZ
+        L.cda_prefill_workspace_size.argtypes = [_I32, _I32, _I32, _I32, _I32, _I32]
+        L.cda_prefill_paged_hadamard_ws.restype = _I32
+        L.cda_prefill_paged_hadamard_ws.argtypes = [
+            _P, _P, _I64, _I32, _I32, _P, _I32, _P, _P, _I32, _P, _P, _I32, _P, _I32, _I32,
+            _I32, _I32, _I32, _F32, _P, _SZ, _P]
         L.cda_fa2_varlen_fwd_hadamard.restype = _I32
         L.cda_fa2_varlen_fwd_hadamard.argtypes = [
             _P, _P, _P, _P, _P, _P, _P, _I32, _I32, _I32, _I32, _I32, _I32, _F32, _P]
@@ -297,9 +305,15 @@ def _check_paged(kv_cache, block_table, seq_lens, cb_k, cb_v):
 def prefill_paged(q: torch.Tensor, kv_cache: torch.Tensor, block_table: torch.Tensor,
                   cu_seqlens_q: torch.Tensor, seq_lens: torch.Tensor, cb_k: torch.Tensor,
                   cb_v: torch.Tensor, out: torch.Tensor, *, block_size: int,
-                  max_query_len: int, scale: float) -> None:
+                  max_query_len: int, scale: float, max_seq_len: int | None = None,
+                  workspace: torch.Tensor | None = None) -> None:
     """Causal varlen prefill straight from the compressed paged cache with the
-    Hadamard prologue/epilogue; ``out`` (T, H_q, 128) fp16 is written in place."""
+    Hadamard prologue/epilogue; ``out`` (T, H_q, 128) fp16 is written in place.
+
+    With ``max_seq_len`` (an upper bound of ``seq_lens``) short query chunks
+    over long contexts split their keys over more workgroups
+    (``cda_prefill_paged_hadamard_ws``); ``workspace`` (uint8, reused when large
+    enough) holds the partials, else one is allocated."""
     dev = _require_gpu(q, kv_cache, block_table, cu_seqlens_q, seq_lens, cb_k, cb_v, out)
     if q.dtype != torch.float16 or out.dtype != torch.float16:
         raise TypeError("Q and output must be fp16")
@@ -315,12 +329,34 @@ def prefill_paged(q: torch.Tensor, kv_cache: torch.Tensor, block_table: torch.Te
     if seq_lens.numel() < B or block_table.shape[0] < B:
         raise ValueError("seq_lens / block_table have fewer rows than cu_seqlens_q")
     num_slots, H_kv, slot_bytes = kv_cache.shape
-    rc = lib().cda_prefill_paged_hadamard(
+    need = 0
+    if max_seq_len is not None:
+        need = prefill_workspace_size(B, T, H_q, H_kv, int(max_query_len), int(max_seq_len))
+    if need == 0:
+        rc = lib().cda_prefill_paged_hadamard(
+            _ptr(q), _ptr(kv_cache), num_slots, slot_bytes, H_kv, _ptr(block_table),
+            block_table.stride(0), _ptr(cu_seqlens_q), _ptr(seq_lens), B,
+            _ptr(cb_k.float().contiguous()), _ptr(cb_v.float().contiguous()), 16, _ptr(out), T,
+            H_q, int(block_size), int(max_query_len), float(scale), _stream(dev))
+        _check(rc, "cda_prefill_paged_hadamard")
+        return
+    if workspace is None or workspace.numel() < need + 256 or workspace.device != dev:
+        workspace = torch.empty(need + 256, dtype=torch.uint8, device=dev)
+    ws_ptr = workspace.data_ptr()
+    pad = (-ws_ptr) % 256
+    rc = lib().cda_prefill_paged_hadamard_ws(
         _ptr(q), _ptr(kv_cache), num_slots, slot_bytes, H_kv, _ptr(block_table),
         block_table.stride(0), _ptr(cu_seqlens_q), _ptr(seq_lens), B,
         _ptr(cb_k.float().contiguous()), _ptr(cb_v.float().contiguous()), 16, _ptr(out), T, H_q,
-        int(block_size), int(max_query_len), float(scale), _stream(dev))
-    _check(rc, "cda_prefill_paged_hadamard")
+        int(block_size), int(max_query_len), int(max_seq_len), float(scale),
+        ctypes.c_void_p(ws_ptr + pad), workspace.numel() - pad, _stream(dev))
+    _check(rc, "cda_prefill_paged_hadamard_ws")
+
+
+def prefill_workspace_size(B: int, T: int, H_q: int, H_kv: int, max_query_len: int,
+                           max_seq_len: int) -> int:
+    """Bytes of scratch the key-split prefill needs (0: it would not split)."""
+    return int(lib().cda_prefill_workspace_size(B, T, H_q, H_kv, max_query_len, max_seq_len))
 
 
 def fa2_varlen_fwd_hadamard(q: torch.Tensor, k_rot: torch.Tensor, v_rot: torch.Tensor,

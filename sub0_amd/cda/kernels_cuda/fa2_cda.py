@@ -155,7 +155,8 @@ def fa2_cda_prefill_varlen_v1(
         load_fa2_cda_varlen_fused()      # same artefact family as the reference's fused path
         _native.prefill_paged(Q_in.contiguous(), kv, bt, cu_q.contiguous(), sl.contiguous(),
                               cb_K, cb_V, out, block_size=int(block_size),
-                              max_query_len=int(max_query_len), scale=float(scale))
+                              max_query_len=int(max_query_len), scale=float(scale),
+                              max_seq_len=int(max_seq_len))
     if out is not output:
         output.copy_(out)
     if return_dense_kv:

@@ -153,6 +153,14 @@ struct PrefillParams {
     // dense source
     const uint16_t *k_rot, *v_rot;
     const int32_t *cu_k;        // (B+1,) first dense row of each sequence
+    // key split (n_ksplit > 1): split ks of a query block takes key tiles
+    // [ks * ksplit_tiles, +ksplit_tiles) and writes unnormalised partials
+    // (rotated frame) instead of out; prefill_combine_kernel merges them.
+    int n_ksplit;               // 1 = no split
+    int ksplit_tiles;
+    int T_total;                // rows of q / out
+    float *part_o;              // (n_ksplit, T, H_q, 128) fp32
+    float *part_ml;             // (n_ksplit, T, H_q, 2): m (log2 domain), l
 };
 
 // Registers holding one tile's share of the source data for this thread:
@@ -309,7 +317,7 @@ __device__ __forceinline__ void store_tile(const TileRegs &r, uint8_t *kt, uint8
         *reinterpret_cast<uint2 *>(vt + (4 * cv + k) * kVRow + vo) = make_uint2(vw[k][0], vw[k][1]);
 }
 
-template <bool PAGED, int GS>
+template <bool PAGED, int GS, bool KSPLIT = false>
 __global__ void __launch_bounds__(kThreads, 1)
 prefill_kernel(PrefillParams p) {
     __shared__ __align__(16) uint8_t smem[kPrefillLds];
@@ -334,6 +342,8 @@ prefill_kernel(PrefillParams p) {
     }
     const int b = (int)ly;
     const int h = (int)lz;
+    const int ks = KSPLIT ? (int)lx % p.n_ksplit : 0;   // key split (splits of a block adjacent)
+    if (KSPLIT) lx /= (uint32_t)p.n_ksplit;
     const int tid = threadIdx.x;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int lane = tid & 63;
@@ -347,7 +357,7 @@ prefill_kernel(PrefillParams p) {
     // Consecutive workgroups share one (sequence, KV head) and so read the
     // same keys: ordering the grid by causal work across sequences instead
     // was measured 30-40 % slower (the L2 working set grows).
-    const int q0 = (int)(gridDim.x - 1 - lx) * QB;
+    const int q0 = (int)((KSPLIT ? gridDim.x / p.n_ksplit : gridDim.x) - 1 - lx) * QB;
     if (q0 >= seq_q) return;
     const int off = seq_k - seq_q;                   // bottom-right causal alignment
     const int q_last = min(q0 + QB, seq_q) - 1;
@@ -511,24 +521,28 @@ prefill_kernel(PrefillParams p) {
     };
 
     const int ntiles = (kend + kBN - 1) / kBN;
+    // This workgroup's key tiles [jt0, jt1): all of them, or one split's share.
+    const int jt0 = KSPLIT ? min(ntiles, ks * p.ksplit_tiles) : 0;
+    const int jt1 = KSPLIT ? min(ntiles, jt0 + p.ksplit_tiles) : ntiles;
     const int32_t *bt_row = PAGED ? p.block_table + (int64_t)b * p.bt_stride : nullptr;
     const int64_t dense_row0 = PAGED ? 0 : p.cu_k[b];
     TileRegs cur;
     TileRows rows_next{0, 0};
-    if (ntiles > 0) {
-        load_tile<PAGED>(p, cur, fetch_rows<PAGED>(p, bt_row, 0, min(kBN, kend), tid),
-                         dense_row0, h, 0, min(kBN, kend), tid);
-        if (ntiles > 1) rows_next = fetch_rows<PAGED>(p, bt_row, kBN, min(kBN, kend - kBN), tid);
+    if (jt0 < jt1) {
+        const int k0 = jt0 * kBN, k1 = k0 + kBN;
+        load_tile<PAGED>(p, cur, fetch_rows<PAGED>(p, bt_row, k0, min(kBN, kend - k0), tid),
+                         dense_row0, h, k0, min(kBN, kend - k0), tid);
+        if (jt0 + 1 < jt1) rows_next = fetch_rows<PAGED>(p, bt_row, k1, min(kBN, kend - k1), tid);
     }
     __syncthreads();   // tables visible
 
-    for (int j = 0; j < ntiles; ++j) {
+    for (int j = jt0; j < jt1; ++j) {
         uint8_t *buf = smem + (j & 1) * kTileBytes;
         store_tile<PAGED>(cur, buf, buf + kKTile, lutk, lutv, tid);
-        if (j + 1 < ntiles) {
+        if (j + 1 < jt1) {
             const int k1 = (j + 1) * kBN, k2 = (j + 2) * kBN;
             load_tile<PAGED>(p, cur, rows_next, dense_row0, h, k1, min(kBN, kend - k1), tid);
-            if (j + 2 < ntiles) rows_next = fetch_rows<PAGED>(p, bt_row, k2, min(kBN, kend - k2), tid);
+            if (j + 2 < jt1) rows_next = fetch_rows<PAGED>(p, bt_row, k2, min(kBN, kend - k2), tid);
         }
         __syncthreads();
         const int kbase = j * kBN;
@@ -537,6 +551,25 @@ prefill_kernel(PrefillParams p) {
         else tile(buf, kbase, std::true_type{});
     }
     if (!wave_live) return;
+
+    if (KSPLIT) {
+        // Partial of this split: O^T rows are dims (acc element i of tile T is
+        // dim 32T + 8(i >> 2) + 4u + (i & 3)), columns queries.  A split that
+        // saw no visible key writes O = 0, m = -inf, l = 0.
+        if (qw0 + c32 < seq_q) {
+            const int64_t row = ((int64_t)ks * p.T_total + q_begin + qw0 + c32) * p.H_q + hq;
+            float *po = p.part_o + row * kD;
+#pragma unroll
+            for (int T = 0; T < 4; ++T)
+#pragma unroll
+                for (int gi = 0; gi < 4; ++gi)
+                    *reinterpret_cast<float4 *>(po + 32 * T + 8 * gi + 4 * u) =
+                        make_float4(o[T][4 * gi + 0], o[T][4 * gi + 1], o[T][4 * gi + 2],
+                                    o[T][4 * gi + 3]);
+            if (u == 0) *reinterpret_cast<float2 *>(p.part_ml + row * 2) = make_float2(m_run, l_run);
+        }
+        return;
+    }
 
     // ---- epilogue: O_rot = fp16(O / l) (attention.py:93), out = fp16(O_rot H / sqrt(128)).
     const float inv_l = 1.0f / fmaxf(l_run, 1e-30f);
@@ -668,17 +701,130 @@ hadamard128_kernel(const uint16_t *x, uint16_t *y, int64_t rows, float scale) {
     }
 }
 
+// Merge of the key-split partials of prefill_kernel, then the epilogue of the
+// unsplit kernel: O_rot = fp16(O / l) (attention.py:93), out = fp16(O_rot H /
+// sqrt(128)) (compression.py:293-296).  Merge as attention.py:239-272 with m
+// in the log2 domain: w_i = 2^(m_i - max m), O = sum w_i O_i, l = sum w_i l_i.
+// One wave per (token, q-head), two dims per lane; block = 4 q-heads.  Lane i
+// loads split i's (m, l) (n_ksplit <= 64), so the weights come from two wave
+// reductions, and the O loads are issued 16 splits at a time.
+constexpr int kCombineBatch = 16;
+__global__ void __launch_bounds__(256)
+prefill_combine_kernel(const float *__restrict__ part_o, const float *__restrict__ part_ml,
+                       uint16_t *__restrict__ out, int T, int H_q, int n_ksplit) {
+    __shared__ float obs[4][kD];
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int hq = blockIdx.x * 4 + wave;
+    const int t = blockIdx.y;
+    const int64_t split_rows = (int64_t)T * H_q;
+    const int64_t row = (int64_t)t * H_q + hq;
+    float mi = -INFINITY, li = 0.0f;
+    if (lane < n_ksplit) {
+        const float2 ml = *reinterpret_cast<const float2 *>(part_ml + (lane * split_rows + row) * 2);
+        mi = ml.x;
+        li = ml.y;
+    }
+    float m = mi;
+#pragma unroll
+    for (int d = 32; d >= 1; d >>= 1) m = fmaxf(m, __shfl_xor(m, d));
+    // A split without a visible key (m_i = -inf) has weight 0.
+    const float wi = (mi == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(mi - m);
+    float l = wi * li;
+#pragma unroll
+    for (int d = 32; d >= 1; d >>= 1) l += __shfl_xor(l, d);
+    float o0 = 0.0f, o1 = 0.0f;
+    const float *po = part_o + row * kD + 2 * lane;
+    for (int i0 = 0; i0 < n_ksplit; i0 += kCombineBatch) {
+        float2 ov[kCombineBatch];
+#pragma unroll
+        for (int k = 0; k < kCombineBatch; ++k)
+            ov[k] = (i0 + k < n_ksplit)
+                        ? *reinterpret_cast<const float2 *>(po + (i0 + k) * split_rows * kD)
+                        : make_float2(0.0f, 0.0f);
+#pragma unroll
+        for (int k = 0; k < kCombineBatch; ++k) {
+            if (i0 + k >= n_ksplit) break;
+            const float w = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wi), i0 + k));
+            if (w != 0.0f) {
+                o0 = fmaf(w, ov[k].x, o0);
+                o1 = fmaf(w, ov[k].y, o1);
+            }
+        }
+    }
+    const float inv_l = 1.0f / fmaxf(l, 1e-30f);
+    obs[wave][2 * lane] = (float)(_Float16)(o0 * inv_l);
+    obs[wave][2 * lane + 1] = (float)(_Float16)(o1 * inv_l);
+    __syncthreads();
+    // out[j] = sum_k (-1)^popcount(j & k) O_rot[k] / sqrt(128) (Sylvester order).
+    const int j0 = 2 * lane, j1 = 2 * lane + 1;
+    float a0 = 0.0f, a1 = 0.0f;
+#pragma unroll 8
+    for (int k = 0; k < kD; ++k) {
+        const float x = obs[wave][k];
+        a0 += (__builtin_popcount(j0 & k) & 1) ? -x : x;
+        a1 += (__builtin_popcount(j1 & k) & 1) ? -x : x;
+    }
+    const float hs = 0.08838834764831845f;
+    typedef _Float16 half2_ __attribute__((ext_vector_type(2)));
+    const half2_ hv = {(_Float16)(a0 * hs), (_Float16)(a1 * hs)};
+    *reinterpret_cast<half2_ *>(out + row * kD + 2 * lane) = hv;
+}
+
 template <bool PAGED>
 int launch_prefill(const PrefillParams &p, int B, int max_q, hipStream_t st, const char *fn) {
     const int qb = 32 * (kWaves / p.GS);
-    const dim3 grid((max_q + qb - 1) / qb, B, p.H_kv);
+    const dim3 grid((unsigned)((max_q + qb - 1) / qb * p.n_ksplit), B, p.H_kv);
     if (grid.x == 0) return CDA_OK;
-    if (p.GS == 4)
+    if (PAGED && p.n_ksplit > 1) {
+        if (p.GS == 4)
+            prefill_kernel<PAGED, 4, true><<<grid, kThreads, 0, st>>>(p);
+        else
+            prefill_kernel<PAGED, 8, true><<<grid, kThreads, 0, st>>>(p);
+    } else if (p.GS == 4) {
         prefill_kernel<PAGED, 4><<<grid, kThreads, 0, st>>>(p);
-    else
+    } else {
         prefill_kernel<PAGED, 8><<<grid, kThreads, 0, st>>>(p);
+    }
     CDA_LAUNCH_CHECK(std::string(fn) + ": prefill_kernel");
+    if (p.n_ksplit > 1) {
+        prefill_combine_kernel<<<dim3((unsigned)(p.H_q / 4), (unsigned)p.T_total), 256, 0, st>>>(
+            p.part_o, p.part_ml, p.out, p.T_total, p.H_q, p.n_ksplit);
+        CDA_LAUNCH_CHECK(std::string(fn) + ": prefill_combine_kernel");
+    }
     return CDA_OK;
+}
+
+// Key-split plan: split only when the unsplit grid leaves CUs idle (fewer
+// than 256 workgroups), into splits of at least 4 key tiles (256 keys), aiming
+// at one round of ~256 workgroups (one per CU: the kernel's LDS admits one);
+// at most kMaxKsplit splits.  Targets of 512 and 1024 workgroups (two and four
+// rounds of shorter splits) measured 5-30 % slower.
+constexpr int kMaxKsplit = 64;
+static_assert(kMaxKsplit <= 64, "prefill_combine_kernel: one lane per split");
+void prefill_ksplit_plan(int B, int H_q, int H_kv, int max_q, int max_k, int *n_split,
+                         int *split_tiles) {
+    const int qb = 32 * (kWaves / (H_q / H_kv));
+    const int64_t wgs = (int64_t)((max_q + qb - 1) / qb) * B * H_kv;
+    const int tiles = (max_k + kBN - 1) / kBN;
+    int ns = 1;
+    if (wgs > 0 && wgs < 256) {
+        ns = (int)std::min<int64_t>((256 + wgs - 1) / wgs, tiles / 4);
+        ns = std::min(ns, kMaxKsplit);
+    }
+    if (ns < 2) {
+        *n_split = 1;
+        *split_tiles = tiles;
+        return;
+    }
+    const int per = (tiles + ns - 1) / ns;
+    *split_tiles = per;
+    *n_split = (tiles + per - 1) / per;
+}
+
+size_t prefill_ws_bytes(int T, int H_q, int n_split) {
+    const size_t o = (size_t)n_split * T * H_q * kD * 4;
+    const size_t ml = (size_t)n_split * T * H_q * 2 * 4;
+    return ((o + 255) & ~(size_t)255) + ((ml + 255) & ~(size_t)255);
 }
 
 }  // namespace
@@ -686,16 +832,15 @@ int launch_prefill(const PrefillParams &p, int B, int max_q, hipStream_t st, con
 
 using namespace cda;
 
-extern "C" int cda_prefill_paged_hadamard(const void *q, const void *kv_cache, int64_t num_slots,
-                                          int slot_bytes, int H_kv, const int32_t *block_table,
-                                          int bt_stride, const int32_t *cu_seqlens_q,
-                                          const int32_t *seq_lens, int B, const float *cb_k,
-                                          const float *cb_v, int levels, void *out, int T,
-                                          int H_q, int block_size, int max_query_len,
-                                          float scale, void *stream) {
-    const char *fn = "cda_prefill_paged_hadamard";
-    (void)num_slots;
-    (void)T;
+namespace cda {
+namespace {
+// Both paged entry points; max_seq_len < 0: no key split.
+int prefill_paged_impl(const char *fn, const void *q, const void *kv_cache, int slot_bytes,
+                       int H_kv, const int32_t *block_table, int bt_stride,
+                       const int32_t *cu_seqlens_q, const int32_t *seq_lens, int B,
+                       const float *cb_k, const float *cb_v, int levels, void *out, int T,
+                       int H_q, int block_size, int max_query_len, float scale, int max_seq_len,
+                       void *workspace, size_t workspace_bytes, void *stream) {
     CDA_REQUIRE(q && kv_cache && block_table && cu_seqlens_q && seq_lens && cb_k && cb_v && out,
                 "cda_prefill_paged_hadamard: null pointer argument");
     CDA_REQUIRE(B >= 0 && H_kv > 0 && H_q > 0 && max_query_len >= 0,
@@ -728,7 +873,69 @@ extern "C" int cda_prefill_paged_hadamard(const void *q, const void *kv_cache, i
     p.row_bytes = (int64_t)H_kv * slot_bytes;
     p.cb_k = cb_k;
     p.cb_v = cb_v;
+    p.n_ksplit = 1;
+    p.T_total = T;
+    if (max_seq_len >= 0) {
+        int ns, per;
+        prefill_ksplit_plan(B, H_q, H_kv, max_query_len, max_seq_len, &ns, &per);
+        if (ns > 1) {
+            CDA_REQUIRE(T > 0, std::string(fn) + ": T must be the number of query rows");
+            const size_t need = prefill_ws_bytes(T, H_q, ns);
+            if (!workspace || workspace_bytes < need || ((uintptr_t)workspace & 255))
+                return fail(CDA_E_WORKSPACE, std::string(fn) + ": workspace missing, misaligned "
+                                             "or smaller than cda_prefill_workspace_size()");
+            const size_t o_bytes = ((size_t)ns * T * H_q * kD * 4 + 255) & ~(size_t)255;
+            p.n_ksplit = ns;
+            p.ksplit_tiles = per;
+            p.part_o = static_cast<float *>(workspace);
+            p.part_ml = reinterpret_cast<float *>(static_cast<char *>(workspace) + o_bytes);
+        }
+    }
     return launch_prefill<true>(p, B, max_query_len, static_cast<hipStream_t>(stream), fn);
+}
+}  // namespace
+}  // namespace cda
+
+extern "C" int cda_prefill_paged_hadamard(const void *q, const void *kv_cache, int64_t num_slots,
+                                          int slot_bytes, int H_kv, const int32_t *block_table,
+                                          int bt_stride, const int32_t *cu_seqlens_q,
+                                          const int32_t *seq_lens, int B, const float *cb_k,
+                                          const float *cb_v, int levels, void *out, int T,
+                                          int H_q, int block_size, int max_query_len,
+                                          float scale, void *stream) {
+    (void)num_slots;
+    return prefill_paged_impl("cda_prefill_paged_hadamard", q, kv_cache, slot_bytes, H_kv,
+                              block_table, bt_stride, cu_seqlens_q, seq_lens, B, cb_k, cb_v,
+                              levels, out, T, H_q, block_size, max_query_len, scale, -1, nullptr,
+                              0, stream);
+}
+
+extern "C" size_t cda_prefill_workspace_size(int B, int T, int H_q, int H_kv, int max_query_len,
+                                             int max_seq_len) {
+    if (B <= 0 || T <= 0 || H_q <= 0 || H_kv <= 0 || H_q % H_kv != 0 ||
+        (H_q / H_kv != 4 && H_q / H_kv != 8) || max_query_len <= 0 || max_seq_len <= 0)
+        return 0;
+    int ns, per;
+    prefill_ksplit_plan(B, H_q, H_kv, max_query_len, max_seq_len, &ns, &per);
+    return ns > 1 ? prefill_ws_bytes(T, H_q, ns) : 0;
+}
+
+extern "C" int cda_prefill_paged_hadamard_ws(const void *q, const void *kv_cache,
+                                             int64_t num_slots, int slot_bytes, int H_kv,
+                                             const int32_t *block_table, int bt_stride,
+                                             const int32_t *cu_seqlens_q, const int32_t *seq_lens,
+                                             int B, const float *cb_k, const float *cb_v,
+                                             int levels, void *out, int T, int H_q,
+                                             int block_size, int max_query_len, int max_seq_len,
+                                             float scale, void *workspace,
+                                             size_t workspace_bytes, void *stream) {
+    const char *fn = "cda_prefill_paged_hadamard_ws";
+    (void)num_slots;
+    CDA_REQUIRE(max_seq_len >= 0, "cda_prefill_paged_hadamard_ws: max_seq_len must be >= 0");
+    return prefill_paged_impl(fn, q, kv_cache, slot_bytes, H_kv, block_table, bt_stride,
+                              cu_seqlens_q, seq_lens, B, cb_k, cb_v, levels, out, T, H_q,
+                              block_size, max_query_len, scale, max_seq_len, workspace,
+                              workspace_bytes, stream);
 }
 
 extern "C" int cda_fa2_varlen_fwd_hadamard(const void *q, const void *k_rot, const void *v_rot,
@@ -761,6 +968,8 @@ extern "C" int cda_fa2_varlen_fwd_hadamard(const void *q, const void *k_rot, con
     p.k_rot = static_cast<const uint16_t *>(k_rot);
     p.v_rot = static_cast<const uint16_t *>(v_rot);
     p.cu_k = cu_seqlens_k;
+    p.n_ksplit = 1;
+    p.T_total = T;
     return launch_prefill<false>(p, B, max_query_len, static_cast<hipStream_t>(stream), fn);
 }
 

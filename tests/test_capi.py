@@ -38,6 +38,24 @@ def test_version_and_plan():
     assert 0 < ws1 <= ws2 and ws1 % 256 == 0
 
 
+def test_prefill_key_split_plan():
+    """Host-side plan of the key-split prefill: split only short chunks over
+    long contexts (grid under 256 workgroups, >= 4 key tiles per split, <= 64
+    splits); the workspace holds (O, m, l) per split, query row and q-head."""
+    from sub0_amd import _native
+    ws = _native.prefill_workspace_size
+    # 16 queries over 16K keys, 8 KV heads: 8 workgroups -> 32 splits of 8 tiles.
+    assert ws(1, 16, 32, 8, 16, 16384) == 32 * 16 * 32 * 128 * 4 + 32 * 16 * 32 * 2 * 4
+    # 1 query over 64K keys, 1 KV head: 1 workgroup -> min(256, 1024 // 4) -> 64 (the cap).
+    assert ws(1, 1, 4, 1, 1, 65536) == 64 * 1 * 4 * 128 * 4 + 64 * 1 * 4 * 2 * 4
+    # 4000 keys = 63 tiles: min(64, 63 // 4) = 15 splits -> 5 tiles each -> 13 splits.
+    assert ws(1, 16, 32, 8, 16, 4000) == 13 * 16 * 32 * 128 * 4 + 13 * 16 * 32 * 2 * 4
+    assert ws(1, 16, 32, 8, 16, 200) == 0            # too few keys to split
+    assert ws(8, 8 * 4096, 32, 8, 4096, 8192) == 0   # config-3-sized grid fills the chip
+    assert ws(0, 0, 32, 8, 16, 16384) == 0
+    assert ws(1, 16, 32, 5, 16, 16384) == 0          # group size not 4 or 8
+
+
 def test_invalid_arguments_are_rejected_before_launch():
     from sub0_amd import _native
     L = _native.lib()

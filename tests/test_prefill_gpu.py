@@ -21,7 +21,7 @@ def _dev(x, dev):
     return torch.from_numpy(np.ascontiguousarray(x)).to(dev)
 
 
-def run_prefill(case, dev, *, dense=False, scale=None):
+def run_prefill(case, dev, *, dense=False, scale=None, split=False):
     from sub0_amd import _native
     q = _dev(case.q, dev)
     out = torch.full_like(q, float("nan"))
@@ -40,7 +40,8 @@ def run_prefill(case, dev, *, dense=False, scale=None):
         _native.fa2_varlen_fwd_hadamard(q, k_rot, v_rot, out, cu, cu_k, sk, max_q, max_k, sc)
     else:
         _native.prefill_paged(q, cache, bt, cu, sk, cb, cb, out, block_size=case.block_size,
-                              max_query_len=max_q, scale=sc)
+                              max_query_len=max_q, scale=sc,
+                              max_seq_len=max_k if split else None)
     torch.cuda.synchronize()
     return out.cpu().numpy()
 
@@ -177,3 +178,36 @@ def test_dropin_prefill_wrapper(gpu):
         torch.cuda.synchronize()
         check(out.cpu().numpy(), case.expected)
         assert (r is not None) == dense
+
+
+# Key-split prefill (cda_prefill_paged_hadamard_ws): short query chunks over long
+# contexts; ragged key lengths leave some splits without keys.
+SPLIT_CASES = [
+    # name, seq_q, seq_k, H_kv, gs
+    ("short_chunk", [16], [4000], 8, 4),
+    ("ragged", [5, 30, 1], [700, 2000, 1500], 8, 4),
+    ("gs8", [20], [3000], 4, 8),
+    ("one_token", [1, 1], [1, 1200], 8, 4),
+    ("chunk_not_multiple", [40], [2333], 8, 4),
+]
+
+
+@pytest.mark.parametrize("name,seq_q,seq_k,H_kv,gs", SPLIT_CASES, ids=[c[0] for c in SPLIT_CASES])
+def test_prefill_key_split_matches_checker(gpu, name, seq_q, seq_k, H_kv, gs):
+    from sub0_amd import _native
+    print(f"[prefill-split] case={name} seq_q={seq_q} seq_k={seq_k}", flush=True)
+    case = make_prefill_case(4700 + len(name), seq_q, seq_k, H_kv=H_kv, gs=gs, fill=0xFF)
+    T = int(case.cu_q[-1])
+    need = _native.prefill_workspace_size(len(seq_q), T, H_kv * gs, H_kv, max(seq_q), max(seq_k))
+    assert need > 0, "the case is meant to take the key-split path"
+    out = run_prefill(case, gpu, split=True)
+    check(out, case.expected)
+    ref = run_prefill(case, gpu)           # unsplit kernel on the same cache
+    assert float(np.abs(out.astype(np.float32) - ref.astype(np.float32)).max()) <= 1e-3
+
+
+def test_prefill_key_split_negative_scale(gpu):
+    print("[prefill-split] negative scale", flush=True)
+    case = make_prefill_case(4800, [12], [2500], H_kv=8, gs=4, scale=-0.15)
+    out = run_prefill(case, gpu, scale=-0.15, split=True)
+    check(out, case.expected)
