@@ -787,6 +787,7 @@ int launch_prefill(const PrefillParams &p, int B, int max_q, hipStream_t st, con
     }
     CDA_LAUNCH_CHECK(std::string(fn) + ": prefill_kernel");
     if (p.n_ksplit > 1) {
+        // grid.y = T fits: a split grid has < 256 workgroups, so T < 256 * 64.
         prefill_combine_kernel<<<dim3((unsigned)(p.H_q / 4), (unsigned)p.T_total), 256, 0, st>>>(
             p.part_o, p.part_ml, p.out, p.T_total, p.H_q, p.n_ksplit);
         CDA_LAUNCH_CHECK(std::string(fn) + ": prefill_combine_kernel");
