@@ -17,34 +17,30 @@
  *   attention_partial_reference / merge_partials  attention.py:190-272
  *   causal_mask              cda/algorithm/attention.py:46-57
  *
- * Arithmetic contract of the encode (the rounding points follow the
- * reference exactly; the summation orders are pinned so that the HIP kernel
- * reproduces every bit):
- *   1. S_j = sum_i x_i * sign(H_ij) in float64.  Inputs are float16, so every
- *      partial sum is exact and the order does not matter.
- *   2. y_j = S_j * h32 in float64, h32 = fp32(1/sqrt(128)) = 0x3db504f3 (the
- *      entry value of the reference's fp32 Hadamard matrix).
- *   3. x_rot_j = fp16(y_j), round-to-nearest-even from float64 (the
- *      reference rounds its fp32 matmul result to the input dtype,
- *      compression.py:291).
- *   4. ss = sum_j x_rot_j^2 in float64 in the "lane tree" order:
- *      p[l] = x[2l]^2 + x[2l+1]^2 for l in 0..63, then p[l] += p[l^m] for
- *      m = 1, 2, 4, ..., 32.  norm = sqrt(ss) correctly rounded to fp32, then
- *      clamp_min(1e-12f).
- *   5. x_unit = fp32(x_rot) / norm (IEEE fp32 division), clamp to [-1, 1]
+ * Arithmetic contract of the encode (every rounding point and every
+ * accumulation order follows the reference's CPU path, so the indices and
+ * norms are bit-exact; tests/test_oracle_golden.py pins this against all of
+ * the reference-written fixtures):
+ *   1. x_rot_j = fp16(acc_j), acc_j the fp32 fused-multiply-add chain over
+ *      k = 0..127 in order: acc = fmaf(x_k, H[k][j], acc) from acc = 0.  This
+ *      is the accumulation order of the MKL sgemm behind
+ *      torch.matmul(x.float(), H) for two or more rows (compression.py:290;
+ *      a single-row matmul takes MKL's gemv, which rounds differently, but
+ *      the paged encode always rotates H_kv >= 2 rows per token).
+ *   2. norm: sq_j = fp32(x_j * x_j) (no fusion), eight lane accumulators
+ *      a_l = sq_l + sq_{8+l} + ... + sq_{120+l} added in order, then
+ *      s = a_0 + a_1 + ... + a_7 in order, norm = fp32 sqrt(s) correctly
+ *      rounded, then clamp_min(1e-12f) (Tensor.norm(dim=-1) on the CPU,
+ *      compression.py:328).
+ *   3. x_unit = fp32(x_rot) / norm (IEEE fp32 division), clamp to [-1, 1]
  *      with NaN passing through (torch.clamp_ semantics).
- *   6. quantize exactly as compression.py:298-313 does in fp32:
+ *   4. quantize exactly as compression.py:298-313 does in fp32:
  *      upper = #{i : !(cb[i] >= x)} (torch.bucketize, right=False; NaN -> L),
  *      upper = min(upper, L-1); lower = max(upper-1, 0);
  *      idx = |cb[upper]-x| < |x-cb[lower]| ? upper : lower (ties -> lower).
- *   7. pack MSB-first (4-bit: even dim in the high nibble; 2-bit: dim 4j at
+ *   5. pack MSB-first (4-bit: even dim in the high nibble; 2-bit: dim 4j at
  *      bits 7:6).
- * The reference computes step 1-2 with an MKL sgemm and step 4 with
- * Tensor.norm, whose fp32 accumulation orders are not specified; where they
- * round differently from the exact value the two can disagree in the last
- * ulp, which flips an index only for values within ulps of a decision
- * boundary.  tests/test_oracle_golden.py counts and classifies those cases.
- */
+*/
 #include <math.h>
 #include <stdint.h>
 #include <stdlib.h>
@@ -129,27 +125,6 @@ float cda_oracle_f16_to_f32(uint16_t h) { return f16_to_f32(h); }
 
 static const uint32_t H32_BITS = 0x3db504f3u;   /* fp32(1/sqrt(128)) */
 
-static double h32(void) {
-    float f;
-    memcpy(&f, &H32_BITS, 4);
-    return (double)f;
-}
-
-/* Exact Sylvester sign transform in float64: out_j = sum_i x_i sign(H_ij),
-   H_ij = (-1)^popcount(i & j) (compression.py:52-56). */
-static void fwht128_exact(const float *x, double *out) {
-    double t[D];
-    for (int i = 0; i < D; ++i) t[i] = (double)x[i];
-    for (int len = 1; len < D; len <<= 1)
-        for (int i = 0; i < D; i += 2 * len)
-            for (int j = i; j < i + len; ++j) {
-                double a = t[j], b = t[j + len];
-                t[j] = a + b;
-                t[j + len] = a - b;
-            }
-    memcpy(out, t, sizeof(t));
-}
-
 /* compression.py:43-57 -- the fp32 matrix the reference builds. */
 void cda_oracle_hadamard128(float *H) {
     float h;
@@ -210,28 +185,36 @@ void cda_oracle_encode_rows(const uint16_t *x, int64_t rows, const float *cb, in
                             uint8_t *packed, float *norm, uint16_t *xrot) {
     const int bits = (L == 16) ? 4 : 2;
     const int bpr = D * bits / 8;
-    const double hh = h32();
+    float hf;
+    memcpy(&hf, &H32_BITS, 4);
 #pragma omp parallel for schedule(static)
     for (int64_t r = 0; r < rows; ++r) {
         float xf[D];
-        double S[D];
         uint16_t xr[D];
         for (int i = 0; i < D; ++i) xf[i] = f16_to_f32(x[r * D + i]);
-        fwht128_exact(xf, S);
-        for (int j = 0; j < D; ++j) xr[j] = cda_oracle_f64_to_f16(S[j] * hh);
+        for (int j = 0; j < D; ++j) {
+            float acc = 0.0f;
+            for (int k = 0; k < D; ++k) {
+                const float hk = (__builtin_popcount((unsigned)(k & j)) & 1) ? -hf : hf;
+                acc = fmaf(xf[k], hk, acc);
+            }
+            xr[j] = cda_oracle_f32_to_f16(acc);
+        }
         if (xrot) memcpy(xrot + r * D, xr, sizeof(xr));
-        double p[64];
-        for (int l = 0; l < 64; ++l) {
-            double a = (double)f16_to_f32(xr[2 * l]);
-            double b = (double)f16_to_f32(xr[2 * l + 1]);
-            p[l] = a * a + b * b;
+        float lanes[8];
+        for (int l = 0; l < 8; ++l) {
+            const float v = f16_to_f32(xr[l]);
+            lanes[l] = v * v;
         }
-        for (int m = 1; m < 64; m <<= 1) {
-            double q[64];
-            for (int l = 0; l < 64; ++l) q[l] = p[l] + p[l ^ m];
-            memcpy(p, q, sizeof(p));
-        }
-        float nv = sqrt_f64_to_f32_rn(p[0]);
+        for (int c = 1; c < D / 8; ++c)
+            for (int l = 0; l < 8; ++l) {
+                const float v = f16_to_f32(xr[8 * c + l]);
+                const float sq = v * v;
+                lanes[l] = lanes[l] + sq;
+            }
+        float ss = lanes[0];
+        for (int l = 1; l < 8; ++l) ss = ss + lanes[l];
+        float nv = sqrt_f64_to_f32_rn((double)ss);
         if (nv < 1e-12f) nv = 1e-12f;    /* clamp_min(1e-12); NaN passes */
         norm[r] = nv;
         uint8_t idx[D];

@@ -4,20 +4,44 @@
 // Reference contract: cda_paged_encode_fused as bound by
 // cda/kernels_cuda/wrappers.py:127-156; arithmetic of Compressor.encode
 // (cda/algorithm/compression.py:287-335) and pack_4bit / pack_2bit
-// (:163-179, :375-386).
+// (:163-179, :375-386).  The result is bit-identical to the reference's CPU
+// path, which fixes three orders:
 //
-// A 16-lane row of a wave encodes one 128-vector: lane j holds elements
-// 8j..8j+7 (one 16-byte load), so the first three butterfly stages and the
-// first three levels of the norm tree stay in registers; an LDS transpose
-// turns three of the other four butterfly stages into register stages, one
-// crosses lanes (DPP within the row), as do four levels of the norm tree; a
-// wave encodes four vectors of one role (K or V).  The butterfly runs in float64, where every partial sum of fp16 inputs
-// is exact, so the rotated value is rounded once, to fp16, exactly as the
-// reference rounds its fp32 matmul result back to the input dtype.  The
-// squared norm is summed in float64 in a fixed pairwise-tree order (element
-// order) and rounded to fp32 with a correctly rounded square root; the
-// division, clamp and the bucketize-style nearest-centroid search give the
-// reference's fp32 results.
+//  * rotation (compression.py:290-291): x_rot_j = fp16(acc_j) with acc_j the
+//    fp32 fused-multiply-add chain over k = 0..127 in order,
+//    acc = fma(x_k, H[k][j], acc), H[k][j] = (-1)^popcount(k & j) * h,
+//    h = fp32(1/sqrt(128)) (the order of the MKL sgemm behind torch.matmul);
+//  * norm (:328): eight lane sums a_l = sq_l + sq_{8+l} + ... + sq_{120+l}
+//    with sq_j = fp32(x_j * x_j), then a_0 + ... + a_7 in order, a correctly
+//    rounded fp32 square root, clamp_min(1e-12);
+//  * x_unit = fp32(x_rot / norm), clamp to [-1, 1], then the bucketize +
+//    neighbour compare of quantize_unit (:298-313) in fp32.
+//
+// Work layout.  P lanes share one 128-vector (P = 4 for throughput, 16 for
+// small batches); lane r of a group owns the outputs j = r + P*m,
+// m = 0..128/P-1.  The chains of outputs that agree in the low bits of j
+// agree in their first steps: (-1)^popcount(k & j) depends only on the bits
+// of j below the highest set bit of k, so for k < 2^t the chains of j and
+// j + 2^t are equal.  Each lane therefore runs its chains as a binary tree:
+// one chain for k < P (the lane's own sign pattern s(k & r) sits in P
+// registers of signed h), which splits in two at k = P, 2P, ..., 64.  That is
+// 2^7 - ... ~ 2731 fused multiply-adds per lane for P = 4 (10924 per vector,
+// against 16384 for 128 independent chains), every one an exact IEEE fma
+// with the sign folded into the operand, so the chain rounds exactly as the
+// reference's.
+//
+// Quantisation without a division.  For a sorted codebook the reference's
+// index is monotone in u = RN32(x / n): it equals #{i in 1..L-1 : u >= th_i}
+// where th_i is the smallest fp32 in (cb[i-1], cb[i]] for which
+// |RN(cb[i] - u)| < |RN(u - cb[i-1])| (found once per block by bisection over
+// the ordered fp32 bit patterns).  RN32(x / n) >= th holds exactly when
+// x / n >= beta (th even) or x / n > beta (th odd), beta the midpoint of th
+// and its fp32 predecessor; x / n >= beta <=> x >= n * beta, and n * beta
+// (24 x 25 significant bits) is exact in float64.  So each vector gets L-1
+// thresholds in the x domain (rounded up to fp32, where every fp16 x lives)
+// and each element a four-step bisection of compares.  Non-finite norms
+// (an fp16 overflow in x_rot, or NaN input) take the reference's formula
+// with a true division.
 #include "cda_common.h"
 
 namespace cda {
@@ -40,198 +64,306 @@ struct EncodeParams {
     const float *cb_v;
 };
 
-// Lane l reads lane l ^ M's 32-bit value (M = 1, 2, 4, 8) with DPP within its
-// row of 16 lanes, without the LDS crossbar (every source lane exists, so no
-// old value is needed).
-template <int M>
-__device__ __forceinline__ uint32_t xor_lane(uint32_t v) {
-    if constexpr (M == 1) {
-        return __builtin_amdgcn_mov_dpp(v, 0xB1, 0xF, 0xF, true);   // quad_perm 1,0,3,2
-    } else if constexpr (M == 2) {
-        return __builtin_amdgcn_mov_dpp(v, 0x4E, 0xF, 0xF, true);   // quad_perm 2,3,0,1
-    } else if constexpr (M == 4) {
-        // row_half_mirror (lane a of each 8-lane half reads lane 7 - a), then
-        // quad_perm 3,2,1,0 (lane a reads a ^ 3): 7 - (a ^ 3) = a ^ 4.
-        const uint32_t m = __builtin_amdgcn_mov_dpp(v, 0x141, 0xF, 0xF, true);
-        return __builtin_amdgcn_mov_dpp(m, 0x1B, 0xF, 0xF, true);
-    } else {
-        static_assert(M == 8, "lane distance within a row");
-        return __builtin_amdgcn_mov_dpp(v, 0x128, 0xF, 0xF, true);   // row_ror:8
+constexpr int kEncWaves = 4;          // waves 2q, 2q+1: K and V of item group q
+
+// Ordered-integer image of an fp32 value (monotone in the value; -0 < +0).
+__device__ __forceinline__ uint32_t f2key(float f) {
+    const uint32_t b = __float_as_uint(f);
+    return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+__device__ __forceinline__ float key2f(uint32_t k) {
+    return __uint_as_float((k & 0x80000000u) ? (k & 0x7FFFFFFFu) : ~k);
+}
+
+// The neighbour compare of quantize_unit for u in bucket i (lo < u <= hi):
+// true picks the upper centroid.
+__device__ __forceinline__ bool pick_upper(float u, float lo, float hi) {
+    return fabsf(__fsub_rn(hi, u)) < fabsf(__fsub_rn(u, lo));
+}
+
+// Decision threshold i (1 <= i < L) of a sorted codebook in the u domain,
+// expressed as (beta, strict): clamp(u) selects at least level i exactly when
+// u >= beta (u > beta when strict), for every u = RN32(v) with v real.
+// Thresholds at or below -1 always hold after the clamp (beta = -inf);
+// thresholds above 1 never do (beta = +inf).
+__device__ void codebook_threshold(const float *cb, int i, double *beta, int *strict) {
+    const float lo = cb[i - 1], hi = cb[i];
+    uint32_t a = f2key(lo) + 1u, b = f2key(hi);
+    if (a <= b) {
+        while (a < b) {
+            const uint32_t mid = a + ((b - a) >> 1);
+            if (pick_upper(key2f(mid), lo, hi)) b = mid; else a = mid + 1u;
+        }
     }
+    // a: the smallest fp32 above lo that selects i (an empty bucket, lo == hi,
+    // gives nextup(hi): only values above hi select it, as in the reference).
+    const float th = key2f(a);
+    if (th <= -1.0f) { *beta = -__builtin_inf(); *strict = 0; return; }
+    if (th > 1.0f) { *beta = __builtin_inf(); *strict = 0; return; }
+    uint32_t pk = a - 1u;
+    if (__float_as_uint(key2f(pk)) == 0x80000000u && __float_as_uint(th) == 0u) pk -= 1u;  // pred(+0)
+    *beta = ((double)key2f(pk) + (double)th) * 0.5;
+    *strict = (int)(__float_as_uint(th) & 1u);
 }
 
-template <int M>
-__device__ __forceinline__ double xor_lane_d(double v) {
-    const uint64_t b = (uint64_t)__double_as_longlong(v);
-    const uint32_t lo = xor_lane<M>((uint32_t)b);
-    const uint32_t hi = xor_lane<M>((uint32_t)(b >> 32));
-    return __longlong_as_double((long long)(((uint64_t)hi << 32) | lo));
+// Smallest fp32 >= t (t finite or infinite).
+__device__ __forceinline__ float round_up_f32(double t) {
+    float f = (float)t;
+    if ((double)f < t) f = __uint_as_float(__float_as_uint(f) + (f >= 0.0f ? 1u : 0xFFFFFFFFu));
+    return f;
 }
 
-constexpr int kEncWaves = 4;
-
-// Butterfly stage across lanes j, j ^ M (element bit log2(M) + 3): the lower
-// lane keeps x + partner, the upper one partner - x (exact in float64).
-template <int M>
-__device__ __forceinline__ void bfly_lanes(double (&x)[8], int lane) {
-    const double sg = (lane & M) ? -1.0 : 1.0;
-    double pt[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) pt[i] = xor_lane_d<M>(x[i]);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) x[i] = fma(sg, x[i], pt[i]);
+// Next float64 above t (t finite, non-zero).
+__device__ __forceinline__ double next_up(double t) {
+    const long long b = __double_as_longlong(t);
+    return __longlong_as_double(t > 0.0 ? b + 1 : b - 1);
 }
 
-// Nearest centroid of x among the sorted L-entry codebook: bucketize-style
-// upper index upper = min(#{i : !(cb[i] >= x)}, L-1) by bisection (the
-// predicate is monotone in i for a sorted codebook; NaN makes it true
-// everywhere, as in the count), then the neighbour compare: the upper index
-// unless the lower neighbour is at least as close (compression.py:298-313).
-// cbl: the codebook in LDS (probes; one shared copy, so lanes reading
-// different entries hit different banks); tri: (cb[2i-1] (cb[0] for i = 0),
-// cb[2i], cb[2i+1]) triples for the last step and the compare.
+// The reference's quantize_unit on one fp32 value (compression.py:298-313):
+// only used for vectors with a non-finite norm.
 template <int L>
-__device__ __forceinline__ uint32_t quantize_bisect(float x, const float *cbl, const float4 *tri) {
-    int pos = 0;
+__device__ uint32_t quantize_ref(float u, const float *cb) {
+    int upper = 0;
 #pragma unroll
-    for (int step = L / 2; step >= 2; step >>= 1)
-        if (!(cbl[pos + step - 1] >= x)) pos += step;
-    const float4 t = tri[pos >> 1];
-    const bool c1 = !(t.y >= x);
-    const int upper = pos + (c1 ? 1 : 0);
-    const float cu = c1 ? t.z : t.y;
-    const float cl = c1 ? t.y : t.x;
+    for (int i = 0; i < L; ++i) upper += !(cb[i] >= u) ? 1 : 0;
+    upper = upper > L - 1 ? L - 1 : upper;
     const int lower = upper - 1 < 0 ? 0 : upper - 1;
-    const float du = fabsf(cu - x);
-    const float dl = fabsf(x - cl);
+    const float du = fabsf(__fsub_rn(cb[upper], u));
+    const float dl = fabsf(__fsub_rn(u, cb[lower]));
     return (uint32_t)(du < dl ? upper : lower);
 }
 
+// Sixteen thresholds as one register vector (element 0 unused): a vector
+// value, not an array in memory, so the bisection's selects stay selects.
+typedef float ThrVec __attribute__((ext_vector_type(16)));
+
+// #{i : x >= t[i]} for sorted thresholds t[1..L-1] by bisection.
 template <int L>
+__device__ __forceinline__ uint32_t count_ge(float x, ThrVec t) {
+    if constexpr (L == 16) {
+        const bool b3 = x >= t[8];
+        const bool b2 = x >= (b3 ? t[12] : t[4]);
+        const float c1 = b3 ? (b2 ? t[14] : t[10]) : (b2 ? t[6] : t[2]);
+        const bool b1 = x >= c1;
+        const float e0 = b2 ? (b1 ? t[7] : t[5]) : (b1 ? t[3] : t[1]);
+        const float e1 = b2 ? (b1 ? t[15] : t[13]) : (b1 ? t[11] : t[9]);
+        const bool b0 = x >= (b3 ? e1 : e0);
+        return (b3 ? 8u : 0u) | (b2 ? 4u : 0u) | (b1 ? 2u : 0u) | (b0 ? 1u : 0u);
+    } else {
+        static_assert(L == 4, "4 or 16 levels");
+        const bool b1 = x >= t[2];
+        const bool b0 = x >= (b1 ? t[3] : t[1]);
+        return (b1 ? 2u : 0u) | (b0 ? 1u : 0u);
+    }
+}
+
+template <int P>
+struct EncLayout {
+    static constexpr int V = 64 / P;          // vectors per wave
+    static constexpr int M = kD / P;          // outputs per lane
+    static constexpr int kPitch = kD + P;     // floats per vector row in LDS (bank spread)
+    // per wave: V rows of sq / idx, then V x 16 thresholds, V x 8 lane sums
+    static constexpr int kWaveFloats = V * kPitch + V * 16 + V * 8;
+};
+
+template <int L, int P>
 __global__ void __launch_bounds__(64 * kEncWaves)
 paged_encode_kernel(EncodeParams p) {
+    using Lay = EncLayout<P>;
+    constexpr int V = Lay::V, M = Lay::M, PITCH = Lay::kPitch;
     constexpr int KB = kD * (L == 16 ? 4 : 2) / 8;   // code bytes per role
-    __shared__ float4 tri[2][L / 2];
-    __shared__ float cbl[2][L];
-    __shared__ double xt[4 * kEncWaves][kD];      // one 128-vector per 16-lane row
-    if (threadIdx.x < L) {
-        const int r = threadIdx.x / (L / 2), i = threadIdx.x % (L / 2);
-        const float *c = r ? p.cb_v : p.cb_k;
-        tri[r][i] = make_float4(c[i ? 2 * i - 1 : 0], c[2 * i], c[2 * i + 1], 0.0f);
+    __shared__ double s_beta[2][16];
+    __shared__ int s_strict[2][16];
+    __shared__ float s_cb[2][16];
+    __shared__ float s_w[kEncWaves][Lay::kWaveFloats];
+
+    if (threadIdx.x < 2 * L) {
+        const int r = threadIdx.x / L, i = threadIdx.x % L;
+        const float *cb = r ? p.cb_v : p.cb_k;
+        s_cb[r][i] = cb[i];
+        if (i > 0) codebook_threshold(cb, i, &s_beta[r][i], &s_strict[r][i]);
     }
-    if (threadIdx.x < 2 * L)
-        cbl[threadIdx.x / L][threadIdx.x % L] =
-            (threadIdx.x < L ? p.cb_k : p.cb_v)[threadIdx.x % L];
     __syncthreads();
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int role = wave >> 1;                       // waves 0,1: K; 2,3: V (wave-uniform)
-    const int j = lane & 15;
-    // (token, head) item of this row; fewer than 2^31 items (checked on the host).
+    const int role = wave & 1;                        // wave-uniform: 0 = K, 1 = V
+    const int g = lane / P, r = lane % P;
+    float *sq_row = s_w[wave] + g * PITCH;            // this vector's 128 floats
+    float *thr = s_w[wave] + V * PITCH + g * 16;
+    float *lsum = s_w[wave] + V * PITCH + V * 16 + g * 8;
+
+    // (token, head) item of this lane group; fewer than 2^31 items (host check).
     const uint32_t items = (uint32_t)(p.num_tokens * p.H_kv);
-    const uint32_t item = blockIdx.x * 8u + 4u * (uint32_t)(wave & 1) + (uint32_t)(lane >> 4);
+    const uint32_t item = blockIdx.x * (uint32_t)(V * kEncWaves / 2) +
+                          (uint32_t)(wave >> 1) * (uint32_t)V + (uint32_t)g;
     const bool valid = item < items;
     const uint32_t t32 = valid ? item / (uint32_t)p.H_kv : 0u;
     const int h = valid ? (int)(item - t32 * (uint32_t)p.H_kv) : 0;
     const int64_t t = t32;
 
-    double x[8];
+    // ---- load the vector (all P lanes of the group read the same 256 B) ----
+    float x[kD];
     {
         const uint16_t *src = role == 0 ? p.k + t * p.k_stride + (int64_t)h * kD
                                         : p.v + t * p.v_stride + (int64_t)h * kD;
-        uint4 w = make_uint4(0, 0, 0, 0);
-        if (valid) w = reinterpret_cast<const uint4 *>(src)[j];
-        const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+        const uint4 *s4 = reinterpret_cast<const uint4 *>(src);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            x[2 * i] = (double)h2f((uint16_t)(ws[i] & 0xFFFFu));
-            x[2 * i + 1] = (double)h2f((uint16_t)(ws[i] >> 16));
+        for (int q = 0; q < kD / 8; ++q) {
+            uint4 w = make_uint4(0, 0, 0, 0);
+            if (valid) w = s4[q];
+            const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                x[8 * q + 2 * e] = h2f((uint16_t)(ws[e] & 0xFFFFu));
+                x[8 * q + 2 * e + 1] = h2f((uint16_t)(ws[e] >> 16));
+            }
         }
     }
-    // Sylvester butterflies, exact in float64 (so their order is free):
-    // element bits 0-2 in registers; then a transpose through LDS gives lane
-    // j the elements (j & 7) + 8 r + 64 (j >> 3), r = 0..7, so bits 3-5 are
-    // register stages too and only bit 6 crosses lanes (j ^ 8); a second
-    // transpose restores elements 8j..8j+7 to lane j.
-    auto bfly_regs = [&]() CDA_INLINE {
+
+    // ---- rotation: the fma chains as a tree ---------------------------------
+    const float hval = __int_as_float(0x3db504f3);    // fp32(1/sqrt(128))
+    float hs[P];                                      // s(k & r) * h for k mod P
 #pragma unroll
-        for (int m = 1; m < 8; m <<= 1)
-#pragma unroll
-            for (int i = 0; i < 8; ++i)
-                if (!(i & m)) {
-                    const double a = x[i], b = x[i | m];
-                    x[i] = a + b;
-                    x[i | m] = a - b;
-                }
-    };
-    bfly_regs();
+    for (int q = 0; q < P; ++q) hs[q] = (__popc((uint32_t)(q & r)) & 1) ? -hval : hval;
+    float ch[M];
     {
-        double *row = xt[threadIdx.x >> 4];       // this lane's vector (128 doubles)
-        const int e0 = (j & 7) + 64 * (j >> 3);
-        double2 *mine = reinterpret_cast<double2 *>(row + 8 * j);
+        float c = 0.0f;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) mine[i] = make_double2(x[2 * i], x[2 * i + 1]);
-        __builtin_amdgcn_wave_barrier();
+        for (int k = 0; k < P; ++k) c = fmaf(x[k], hs[k], c);
+        ch[0] = c;
+    }
 #pragma unroll
-        for (int r = 0; r < 8; ++r) x[r] = row[e0 + 8 * r];
-        bfly_regs();
-        bfly_lanes<8>(x, lane);
-        __builtin_amdgcn_wave_barrier();
+    for (int lvl = 0; (P << lvl) < kD; ++lvl) {
+        const int cnt = 1 << lvl;                     // chains so far (m mod cnt)
+        const int k0 = P << lvl;                      // steps k0 .. 2 k0 - 1
 #pragma unroll
-        for (int r = 0; r < 8; ++r) row[e0 + 8 * r] = x[r];
-        __builtin_amdgcn_wave_barrier();
+        for (int m = 0; m < cnt; ++m) ch[m + cnt] = ch[m];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const double2 v = mine[i];
-            x[2 * i] = v.x;
-            x[2 * i + 1] = v.y;
+        for (int k = k0; k < 2 * k0; ++k)
+#pragma unroll
+            for (int m = 0; m < 2 * cnt; ++m) {
+                const bool neg = (__builtin_popcount((unsigned)(k & (P * m))) & 1) != 0;
+                ch[m] = fmaf(x[k], neg ? -hs[k % P] : hs[k % P], ch[m]);
+            }
+    }
+
+    // ---- fp16 rounding, squares, norm (reference order) ---------------------
+    float xr[M];
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+        // The fp32 chain value is rounded on its own, then to fp16 (the
+        // reference rounds its fp32 matmul output to the input dtype); the
+        // empty asm keeps the compiler from fusing the last fma with the fp16
+        // conversion into one rounding (v_fma_mixlo_f16).
+        asm volatile("" : "+v"(ch[m]));
+        xr[m] = __half2float(__float2half_rn(ch[m]));
+        sq_row[r + P * m] = __fmul_rn(xr[m], xr[m]);
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+    for (int l0 = 0; l0 < 8; l0 += P) {
+        const int l = l0 + r;
+        if (l < 8) {
+            float a = sq_row[l];
+#pragma unroll
+            for (int c = 1; c < kD / 8; ++c) a = __fadd_rn(a, sq_row[8 * c + l]);
+            lsum[l] = a;
         }
     }
-    const double hsc = (double)__int_as_float(0x3db504f3);   // fp32(1/sqrt(128))
-    float f[8];
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    float ss = lsum[0];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) f[i] = h2f(f64_to_f16_rn(x[i] * hsc));
-    // Squared norm: the pairwise tree in element order.
-    double sq[8];
+    for (int l = 1; l < 8; ++l) ss = __fadd_rn(ss, lsum[l]);
+    float n = sqrt_f64_to_f32_rn((double)ss);
+    n = (n < 1e-12f) ? 1e-12f : n;                    // clamp_min(1e-12); NaN passes
+
+    // ---- per-vector thresholds in the x domain ------------------------------
+    const bool finite_n = fabsf(n) < __builtin_inff();
 #pragma unroll
-    for (int i = 0; i < 8; ++i) sq[i] = (double)f[i] * (double)f[i];
-    double ss = ((sq[0] + sq[1]) + (sq[2] + sq[3])) + ((sq[4] + sq[5]) + (sq[6] + sq[7]));
-    ss = ss + xor_lane_d<1>(ss);
-    ss = ss + xor_lane_d<2>(ss);
-    ss = ss + xor_lane_d<4>(ss);
-    ss = ss + xor_lane_d<8>(ss);
-    float n = sqrt_f64_to_f32_rn(ss);
-    n = (n < 1e-12f) ? 1e-12f : n;     // clamp_min(1e-12); NaN passes through
-    // u = RN32(f / n) as RN32(f * RN64(1 / n)): the float64 product is within
-    // 2^-52 (relative) of f / n, and a quotient of two 24-bit numbers is never
-    // a 25-bit rounding midpoint and, when not one, lies at least 2^-49 from
-    // every midpoint, so the final rounding equals the correctly rounded
-    // quotient (NaN, infinity and zero propagate as in the division).
-    const double rn = 1.0 / (double)n;
-    uint32_t idx[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        float u = (float)((double)f[i] * rn);
-        u = u < -1.0f ? -1.0f : (u > 1.0f ? 1.0f : u);
-        idx[i] = quantize_bisect<L>(u, cbl[role], tri[role]);
+    for (int i0 = 1; i0 < L; i0 += P) {
+        const int i = i0 + r;
+        if (i < L) {
+            const double beta = s_beta[role][i];
+            double tt = (double)n * beta;             // exact: 24 x 25 significant bits
+            if (s_strict[role][i] && finite_n) tt = next_up(tt);
+            thr[i] = round_up_f32(tt);
+        }
     }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    ThrVec tv;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) tv[i] = (i >= 1 && i < L) ? thr[i] : 0.0f;
+
+    // ---- quantise; codes go through LDS (the sq row is free again) ----------
+    uint8_t *idx_row = reinterpret_cast<uint8_t *>(sq_row);
+    uint32_t code[M];
+    if (finite_n) {
+#pragma unroll
+        for (int m = 0; m < M; ++m) code[m] = count_ge<L>(xr[m], tv);
+    } else {
+#pragma unroll
+        for (int m = 0; m < M; ++m) {
+            float u = __fdiv_rn(xr[m], n);
+            u = u < -1.0f ? -1.0f : (u > 1.0f ? 1.0f : u);
+            code[m] = quantize_ref<L>(u, s_cb[role]);
+        }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();                  // lane sums read before the row is reused
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+    for (int m = 0; m < M; ++m) idx_row[r + P * m] = (uint8_t)code[m];
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
     if (!valid) return;
     const int64_t slot = p.slot_mapping[t];
     if (slot < 0 || slot >= p.num_slots) return;
     uint8_t *dst = p.cache + slot * p.row_bytes + (int64_t)h * p.slot_bytes;
     uint8_t *codes = dst + role * KB;
-    if (L == 16) {
-        uint32_t wv = 0;
+    // Lane r packs code bytes [r * KB / P, (r + 1) * KB / P).
+    constexpr int BPL = KB / P;                        // bytes per lane: 16/4 (K4) or 8/2 (K2)
+    constexpr int EPB = L == 16 ? 2 : 4;               // elements per byte
+    const uint32_t *src = reinterpret_cast<const uint32_t *>(idx_row + r * BPL * EPB);
+    uint32_t packed[(BPL + 3) / 4];
 #pragma unroll
-        for (int b = 0; b < 4; ++b) wv |= ((idx[2 * b] << 4) | idx[2 * b + 1]) << (8 * b);
-        *reinterpret_cast<uint32_t *>(codes + 4 * j) = wv;
-    } else {
-        const uint32_t b0 = (idx[0] << 6) | (idx[1] << 4) | (idx[2] << 2) | idx[3];
-        const uint32_t b1 = (idx[4] << 6) | (idx[5] << 4) | (idx[6] << 2) | idx[7];
-        *reinterpret_cast<uint16_t *>(codes + 2 * j) = (uint16_t)(b0 | (b1 << 8));
+    for (int w = 0; w < (BPL + 3) / 4; ++w) packed[w] = 0;
+#pragma unroll
+    for (int b = 0; b < BPL; ++b) {
+        uint32_t byte;
+        if constexpr (L == 16) {
+            const uint32_t e = src[b / 2] >> (16 * (b & 1));      // elements 2b, 2b+1
+            byte = ((e & 0xFu) << 4) | ((e >> 8) & 0xFu);
+        } else {
+            const uint32_t e = src[b];                           // elements 4b .. 4b+3
+            byte = ((e & 3u) << 6) | (((e >> 8) & 3u) << 4) | (((e >> 16) & 3u) << 2) |
+                   ((e >> 24) & 3u);
+        }
+        packed[b / 4] |= byte << (8 * (b & 3));
     }
-    if (j == 0) *reinterpret_cast<float *>(dst + 2 * KB + 4 * role) = n;
+    if constexpr (BPL >= 4) {
+#pragma unroll
+        for (int w = 0; w < BPL / 4; ++w)
+            reinterpret_cast<uint32_t *>(codes + r * BPL)[w] = packed[w];
+    } else {
+        *reinterpret_cast<uint16_t *>(codes + r * BPL) = (uint16_t)packed[0];
+    }
+    if (r == 0) *reinterpret_cast<float *>(dst + 2 * KB + 4 * role) = n;
+}
+
+template <int L, int P>
+void launch_encode(const EncodeParams &p, int64_t items, hipStream_t st) {
+    constexpr int per_block = (64 / P) * kEncWaves / 2;          // items per block
+    const int64_t blocks = (items + per_block - 1) / per_block;
+    paged_encode_kernel<L, P><<<dim3((unsigned)blocks), 64 * kEncWaves, 0, st>>>(p);
 }
 
 }  // namespace
@@ -275,11 +407,15 @@ extern "C" int cda_paged_encode_fused(const void *k, const void *v, int64_t k_st
     const int64_t items = num_tokens * H_kv;
     CDA_REQUIRE(items < ((int64_t)1 << 31), "cda_paged_encode_fused: too many tokens x heads");
     hipStream_t st = static_cast<hipStream_t>(stream);
-    const int64_t blocks = (items + 7) / 8;
-    if (levels == 16)
-        paged_encode_kernel<16><<<dim3((unsigned)blocks), 64 * kEncWaves, 0, st>>>(p);
-    else
-        paged_encode_kernel<4><<<dim3((unsigned)blocks), 64 * kEncWaves, 0, st>>>(p);
+    // Four lanes per vector run the fewest instructions per vector; sixteen
+    // finish a wave four times sooner.  Take 16 while the 4-lane grid would
+    // leave the SIMDs with fewer than two waves each.
+    const bool wide = items * 2 / 16 < 2048;
+    if (levels == 16) {
+        if (wide) launch_encode<16, 16>(p, items, st); else launch_encode<16, 4>(p, items, st);
+    } else {
+        if (wide) launch_encode<4, 16>(p, items, st); else launch_encode<4, 4>(p, items, st);
+    }
     CDA_LAUNCH_CHECK("paged_encode_kernel");
     return CDA_OK;
 }

@@ -104,3 +104,65 @@ def test_encode_config2_scale(gpu, codebooks):
     exp = expected_cache(k, v, slots, cb, num_slots, 144, 0)
     got = run_gpu_encode(gpu, k, v, slots, cb, num_slots, 144, 0)
     assert np.array_equal(got, exp)
+
+
+def test_encode_golden_rows_wide_batch(gpu, golden, codebooks):
+    """The fixture rows repeated into a batch large enough for the 4-lane
+    layout (the one config 2 takes): still the reference's indices and norms,
+    including the zero, subnormal and fp16-overflow edge rows."""
+    e = golden("encode.npz")
+    x = e["x"]
+    rows = x.shape[0]
+    reps = 16
+    xx = np.tile(x, (reps, 1)).reshape(rows * reps // 8, 8, 128)
+    T = xx.shape[0]
+    for levels, tag in ((16, "k4"), (4, "k2")):
+        cb = codebooks["lloyd_beta16" if levels == 16 else "lloyd_beta4"]
+        kb = 64 if levels == 16 else 32
+        sb = 144 if levels == 16 else 80
+        print(f"[encode] golden rows x{reps} levels={levels}", flush=True)
+        got = run_gpu_encode(gpu, xx, xx, np.arange(T), cb, T, sb, 0)
+        codes = got[:, :, :kb].reshape(reps, rows, kb)
+        norms = got[:, :, 2 * kb:2 * kb + 4].copy().view(np.float32).reshape(reps, rows)
+        for i in range(reps):
+            assert np.array_equal(codes[i], e[f"{tag}_idx"])
+            assert np.array_equal(norms[i].view(np.uint32), e[f"{tag}_norm"].view(np.uint32))
+
+
+def test_encode_config0_matches_reference(gpu, golden, codebooks):
+    """BASELINE config 0 (4096 tokens x 8 KV heads, outlier K, N(0,1) V): the
+    GPU encoder writes exactly the reference's k_idx / v_idx and fp32 norms."""
+    import json
+    from pathlib import Path
+    g = golden("attn_cfg0.npz")
+    meta = json.loads((Path(__file__).parent / "golden" / "attn_cfg0.json").read_text())
+    N, H_kv, seed = meta["N"], meta["H_kv"], meta["seed"]
+    cb = codebooks["lloyd_beta16"]
+    k = synth.kv_with_outliers(seed, (1, H_kv, N, 128))[0].transpose(1, 0, 2).copy()
+    v = synth.normal_f16(seed + 1, (1, H_kv, N, 128))[0].transpose(1, 0, 2).copy()
+    print("[encode] config 0 vs reference", flush=True)
+    got = run_gpu_encode(gpu, k, v, np.arange(N), cb, N, 144, 0)
+    kidx = got[:, :, :64].transpose(1, 0, 2)
+    vidx = got[:, :, 64:128].transpose(1, 0, 2)
+    kn = got[:, :, 128:132].copy().view(np.float32)[..., 0].T
+    vn = got[:, :, 132:136].copy().view(np.float32)[..., 0].T
+    assert np.array_equal(kidx, g["k_idx"][0])
+    assert np.array_equal(vidx, g["v_idx"][0])
+    assert np.array_equal(kn.view(np.uint32), g["k_norm"][0].view(np.uint32))
+    assert np.array_equal(vn.view(np.uint32), g["v_norm"][0].view(np.uint32))
+
+
+def test_encode_config2_scale_k2v2(gpu, codebooks):
+    """Config 2 with the 4-level codebook: 64 sequences x U[1,256] new tokens."""
+    cb = codebooks["lloyd_beta4"]
+    rng_lens = (synth._splitmix64(8, 64) % np.uint64(256) + np.uint64(1)).astype(np.int64)
+    T = int(rng_lens.sum())
+    H_kv = 8
+    k = synth.kv_with_outliers(611, (T, H_kv, 128))
+    v = synth.normal_f16(612, (T, H_kv, 128))
+    num_slots = 64 * 256
+    slots = synth.permuted_block_table(613, 1, num_slots)[0][:T].astype(np.int64)
+    print(f"[encode] config 2 K2V2 T={T}", flush=True)
+    exp = expected_cache(k, v, slots, cb, num_slots, 80, 0)
+    got = run_gpu_encode(gpu, k, v, slots, cb, num_slots, 80, 0)
+    assert np.array_equal(got, exp)

@@ -94,20 +94,28 @@ def _round_f16_exact(fr):
     return best[1]
 
 
-def test_encode_rotation_and_norm_are_correctly_rounded(codebooks):
-    """x_rot = fp16 of the exact rotation, norm = fp32 of the exact sqrt of
-    sum(x_rot^2), both checked with rational arithmetic on random rows."""
+def test_encode_rotation_and_norm_within_fp32_error_bounds(codebooks):
+    """x_rot is an fp32 recurrence of 128 fused multiply-adds rounded to fp16,
+    the norm a 128-term fp32 sum of squares: each must lie within the textbook
+    error bound of the exact value (rational arithmetic on random rows), so a
+    dropped term, a wrong sign or a transposed operand fails."""
     x = synth.kv_with_outliers(11, (6, D))
     _, norm, xrot = O.encode(x, codebooks["lloyd_beta16"])
+    u32 = Fraction(1, 2 ** 24)
+    gamma = 128 * u32 / (1 - 128 * u32)
     for r in range(x.shape[0]):
         ex = _exact_row(x[r])
-        want = np.array([_round_f16_exact(v) for v in ex], dtype=np.float16)
-        assert np.array_equal(xrot[r].view(np.uint16), want.view(np.uint16))
-        ss = sum(Fraction(float(v)) ** 2 for v in want)
-        n = np.float32(norm[r])
-        lo = Fraction(float(np.nextafter(n, np.float32(0)))) + Fraction(float(n))
-        hi = Fraction(float(np.nextafter(n, np.float32(np.inf)))) + Fraction(float(n))
-        assert (lo / 2) ** 2 <= ss <= (hi / 2) ** 2
+        h = Fraction(float(np.float32(1 / np.sqrt(128))))
+        abs_sum = sum(abs(Fraction(float(v))) for v in x[r]) * h
+        for j in range(D):
+            got = Fraction(float(xrot[r, j]))
+            ulp16 = Fraction(float(np.spacing(np.float16(abs(xrot[r, j])))))
+            assert abs(got - ex[j]) <= gamma * abs_sum + ulp16 / 2 + Fraction(1, 2 ** 25)
+        ss = sum(Fraction(float(v)) ** 2 for v in xrot[r])
+        n = Fraction(float(norm[r]))
+        # sum of squares: relative error <= gamma_129; sqrt and its rounding <= 2 u32
+        lo, hi = ss * (1 - gamma * 2), ss * (1 + gamma * 2)
+        assert lo * (1 - 4 * u32) <= n * n <= hi * (1 + 4 * u32)
 
 
 def test_encode_decode_round_trip(codebooks):
