@@ -101,10 +101,11 @@ int cda_decode_set_stream_kernel(int enable);
  * slot_mapping:  (T,) int32; a negative slot (vLLM padding) is skipped.
  * flat_cache:    (num_slots, H_kv, slot_bytes) uint8, written in place.
  * cb_k, cb_v:    (levels,) fp32, levels = 16 (K4V4) or 4 (K2V2).
- * Per (token, head, role): Hadamard-128 (exact float64 butterfly, one fp16
- * rounding), fp32 L2 norm clamped to 1e-12, nearest centroid with ties to
- * the lower index (codebooks sorted ascending, as bucketize requires),
- * MSB-first packing (compression.py:315-335).
+ * Per (token, head, role), bit-identical to Compressor.encode
+ * (compression.py:315-335) on the CPU: Hadamard-128 as the fp32 fma chain
+ * over k in order rounded to fp16, fp32 L2 norm in eight ordered lane sums
+ * clamped to 1e-12, nearest centroid with ties to the lower index (codebooks
+ * sorted ascending, as bucketize requires), MSB-first packing.
  */
 int cda_paged_encode_fused(const void *k, const void *v, int64_t k_stride, int64_t v_stride,
                            const int32_t *slot_mapping, int64_t num_tokens, void *flat_cache,
