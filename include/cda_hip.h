@@ -74,6 +74,25 @@ int cda_decode_full_hmma_v3(const void *q, const void *kv_cache, int64_t num_slo
                             int block_size, int tile_n, int max_seq_len, float scale,
                             void *workspace, size_t workspace_bytes, void *stream);
 
+/* Allocation-free variant of cda_decode_full_hmma_v3.  No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code
+ * under graph capture that must not call hipMalloc, tight serving loops,
+ * harnesses that forbid allocation).  Same arguments and result as
+ * cda_decode_full_hmma_v3 without the workspace: the split-K partials go to
+ * a fixed per-GPU device array of the library, of
+ * cda_decode_noalloc_max_workspace() bytes (16 MiB; held until the process
+ * ends).  Shapes whose cda_decode_workspace_size() exceeds it return
+ * CDA_E_WORKSPACE.  It calls no allocator.  Calls on one GPU share the
+ * array: calls that overlap on one GPU (several streams or threads) race. */
+size_t cda_decode_noalloc_max_workspace(void);
+int cda_decode_full_hmma_v3_noalloc(const void *q, const void *kv_cache, int64_t num_slots,
+                                    int slot_bytes, int H_kv, const int32_t *block_table,
+                                    int bt_stride, const int32_t *seq_lens, const float *cb_k,
+                                    const float *cb_v, int levels, const float *rot_f32,
+                                    const void *rot_f16, void *out, int B, int H_q,
+                                    int group_size, int block_size, int tile_n,
+                                    int max_seq_len, float scale, void *stream);
+
 /* Profiling hook, no counterpart in the reference: when both are non-NULL,
  * later cda_decode_full_hmma_v3 calls on this thread record the two hipEvent_t
  * on the launch stream immediately before and after the split-K kernel (the

@@ -29,6 +29,8 @@ SYMBOLS = (
     "cda_decode_full_hmma_v3",
     "cda_decode_set_timing_events",
     "cda_decode_set_stream_kernel",
+    "cda_decode_noalloc_max_workspace",
+    "cda_decode_full_hmma_v3_noalloc",
     "cda_paged_encode_fused",
     "cda_prefill_paged_hadamard",
     "cda_prefill_workspace_size",
@@ -83,6 +85,12 @@ def lib():
         L.cda_decode_full_hmma_v3.argtypes = [
             _P, _P, _I64, _I32, _I32, _P, _I32, _P, _P, _P, _I32, _P, _P, _P,
             _I32, _I32, _I32, _I32, _I32, _I32, _F32, _P, _SZ, _P]
+        L.cda_decode_noalloc_max_workspace.restype = _SZ
+        L.cda_decode_noalloc_max_workspace.argtypes = []
+        L.cda_decode_full_hmma_v3_noalloc.restype = _I32
+        L.cda_decode_full_hmma_v3_noalloc.argtypes = [
+            _P, _P, _I64, _I32, _I32, _P, _I32, _P, _P, _P, _I32, _P, _P, _P,
+            _I32, _I32, _I32, _I32, _I32, _I32, _F32, _P]
         L.cda_decode_set_timing_events.restype = _I32
         L.cda_decode_set_timing_events.argtypes = [_P, _P]
         L.cda_decode_set_stream_kernel.restype = _I32

@@ -25,6 +25,8 @@
 //                 and writes fp16 out.
 #include "cda_common.h"
 
+#include <mutex>
+#include <string>
 #include <type_traits>
 #include <utility>
 
@@ -1325,4 +1327,79 @@ extern "C" int cda_decode_set_timing_events(void *start_event, void *stop_event)
 extern "C" int cda_decode_set_stream_kernel(int enable) {
     g_allow_stream = enable != 0;
     return CDA_OK;
+}
+
+// ------------------------------------------------- allocation-free decode --
+//
+// cda_decode_full_hmma_v3_noalloc: the same decode with the split-K workspace
+// taken from a fixed device array of this library instead of the caller, for
+// callers that cannot allocate (code under graph capture that must not call
+// hipMalloc, tight serving loops, harnesses that forbid allocation).  Every
+// GPU the library runs on holds its own copy of the array until the process
+// ends; every call on one GPU shares it, so calls that overlap on one GPU
+// (two streams, or two threads) race on it.  Nothing in it needs to start at
+// zero: the kernels write q_rot and every split's partials before the
+// combine reads them.
+
+namespace cda {
+namespace {
+
+constexpr size_t kDecodeScratchBytes = size_t(16) << 20;   // 16 MiB per GPU
+__device__ __align__(256) char scratch[kDecodeScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void *g_scratch_ptr[kMaxDevices] = {};
+
+// Device address of `scratch` on the current device (looked up once per
+// device, with that device current).
+int decode_scratch(void **ptr) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices)
+        return fail(CDA_E_HIP, "cda_decode_full_hmma_v3_noalloc: no current HIP device");
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void *p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p)
+            return fail(CDA_E_HIP, std::string("cda_decode_full_hmma_v3_noalloc: "
+                                               "hipGetSymbolAddress(scratch): ") +
+                                       hipGetErrorString(e));
+        g_scratch_ptr[dev] = p;
+    }
+    *ptr = g_scratch_ptr[dev];
+    return CDA_OK;
+}
+
+}  // namespace
+}  // namespace cda
+
+extern "C" size_t cda_decode_noalloc_max_workspace(void) { return cda::kDecodeScratchBytes; }
+
+extern "C" int cda_decode_full_hmma_v3_noalloc(const void *q, const void *kv_cache,
+                                               int64_t num_slots, int slot_bytes, int H_kv,
+                                               const int32_t *block_table, int bt_stride,
+                                               const int32_t *seq_lens, const float *cb_k,
+                                               const float *cb_v, int levels,
+                                               const float *rot_f32, const void *rot_f16,
+                                               void *out, int B, int H_q, int group_size,
+                                               int block_size, int tile_n, int max_seq_len,
+                                               float scale, void *stream) {
+    CDA_REQUIRE(B > 0 && H_kv > 0 && H_q > 0 && max_seq_len >= 0,
+                "cda_decode_full_hmma_v3_noalloc: B, H_q, H_kv must be > 0, max_seq_len >= 0");
+    const size_t need = cda_decode_workspace_size(B, H_q, H_kv, max_seq_len, tile_n);
+    CDA_REQUIRE(need > 0, "cda_decode_full_hmma_v3_noalloc: bad shape or tile_n");
+    if (need > kDecodeScratchBytes)
+        return fail(CDA_E_WORKSPACE,
+                    "cda_decode_full_hmma_v3_noalloc: this shape needs " + std::to_string(need) +
+                        " bytes of split-K scratch, more than the fixed " +
+                        std::to_string(kDecodeScratchBytes) +
+                        "; use cda_decode_full_hmma_v3 with a caller workspace");
+    void *ws = nullptr;
+    const int rc = decode_scratch(&ws);
+    if (rc) return rc;
+    return cda_decode_full_hmma_v3(q, kv_cache, num_slots, slot_bytes, H_kv, block_table,
+                                   bt_stride, seq_lens, cb_k, cb_v, levels, rot_f32, rot_f16,
+                                   out, B, H_q, group_size, block_size, tile_n, max_seq_len,
+                                   scale, ws, kDecodeScratchBytes, stream);
 }
