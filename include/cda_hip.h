@@ -142,7 +142,9 @@ int cda_paged_encode_fused(const void *k, const void *v, int64_t k_stride, int64
  * the pair paged_cache_to_dense_rotated + cda_fa2_varlen_fwd_hadamard that
  * fa2_cda_prefill_varlen_v1(fuse_fa2_epilogue=True) runs
  * (cda/kernels_cuda/fa2_cda.py:98-230).  No single reference symbol.
- *   q, out:        (T, H_q, 128) fp16, unrotated; T = cu_seqlens_q[B].
+ *   q, out:        (T, H_q, 128) fp16, unrotated; T = cu_seqlens_q[B] (a larger
+ *                  T leaves the extra out rows untouched; query rows past T
+ *                  are neither read nor written).
  *   cu_seqlens_q:  (B+1,) int32.   seq_lens: (B,) int32 key lengths.
  *   H_q / H_kv:    4 or 8.         levels: 16.
  *   block_size:    a multiple of 16 (pages of 16 tokens or more).

@@ -227,7 +227,8 @@ def decode(q: torch.Tensor, kv_cache: torch.Tensor, block_table: torch.Tensor,
     cb_k = cb_k.contiguous()
     cb_v = cb_k if _same_codebook(cb_k, cb_v) else cb_v.contiguous()
     need = decode_workspace_size(B, H_q, H_kv, max_seq_len, tile_n)
-    if workspace is None or workspace.numel() < need or workspace.device != dev:
+    if (workspace is None or workspace.device != dev
+            or workspace.numel() - ((-workspace.data_ptr()) % 256) < need):
         workspace = torch.empty(need + 256, dtype=torch.uint8, device=dev)
     ws_ptr = workspace.data_ptr()
     pad = (-ws_ptr) % 256
@@ -348,7 +349,8 @@ def prefill_paged(q: torch.Tensor, kv_cache: torch.Tensor, block_table: torch.Te
             H_q, int(block_size), int(max_query_len), float(scale), _stream(dev))
         _check(rc, "cda_prefill_paged_hadamard")
         return
-    if workspace is None or workspace.numel() < need + 256 or workspace.device != dev:
+    if (workspace is None or workspace.device != dev
+            or workspace.numel() - ((-workspace.data_ptr()) % 256) < need):
         workspace = torch.empty(need + 256, dtype=torch.uint8, device=dev)
     ws_ptr = workspace.data_ptr()
     pad = (-ws_ptr) % 256

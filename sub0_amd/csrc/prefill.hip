@@ -389,7 +389,8 @@ prefill_kernel(PrefillParams p) {
     const uint4 hbase = hadamard_base(c32);
     half8 qb[8];
     {
-        const uint16_t *qrow = p.q + ((int64_t)(q_begin + my_q) * p.H_q + hq) * kD;
+        // Clamped to the T rows of q: a cu_seqlens_q beyond T reads no memory past q.
+        const uint16_t *qrow = p.q + ((int64_t)min(q_begin + my_q, p.T_total - 1) * p.H_q + hq) * kD;
         half8 qin[8];
 #pragma unroll
         for (int S = 0; S < 8; ++S)
@@ -523,7 +524,9 @@ prefill_kernel(PrefillParams p) {
     const int ntiles = (kend + kBN - 1) / kBN;
     // This workgroup's key tiles [jt0, jt1): all of them, or one split's share.
     const int jt0 = KSPLIT ? min(ntiles, ks * p.ksplit_tiles) : 0;
-    const int jt1 = KSPLIT ? min(ntiles, jt0 + p.ksplit_tiles) : ntiles;
+    // The last split runs to the end, so a max_seq_len below some seq_lens[b]
+    // costs speed, never keys.
+    const int jt1 = (KSPLIT && ks < p.n_ksplit - 1) ? min(ntiles, jt0 + p.ksplit_tiles) : ntiles;
     const int32_t *bt_row = PAGED ? p.block_table + (int64_t)b * p.bt_stride : nullptr;
     const int64_t dense_row0 = PAGED ? 0 : p.cu_k[b];
     TileRegs cur;
@@ -556,7 +559,7 @@ prefill_kernel(PrefillParams p) {
         // Partial of this split: O^T rows are dims (acc element i of tile T is
         // dim 32T + 8(i >> 2) + 4u + (i & 3)), columns queries.  A split that
         // saw no visible key writes O = 0, m = -inf, l = 0.
-        if (qw0 + c32 < seq_q) {
+        if (qw0 + c32 < seq_q && q_begin + qw0 + c32 < p.T_total) {
             const int64_t row = ((int64_t)ks * p.T_total + q_begin + qw0 + c32) * p.H_q + hq;
             float *po = p.part_o + row * kD;
 #pragma unroll
@@ -579,7 +582,7 @@ prefill_kernel(PrefillParams p) {
         ob[2 * T] = acc_to_operand(o[T], 0, u, inv_l);
         ob[2 * T + 1] = acc_to_operand(o[T], 1, u, inv_l);
     }
-    const bool store = qw0 + c32 < seq_q;
+    const bool store = qw0 + c32 < seq_q && q_begin + qw0 + c32 < p.T_total;
     uint16_t *orow = p.out + ((int64_t)(q_begin + qw0 + c32) * p.H_q + hq) * kD;
     // A fresh (opaque) copy of the Hadamard base, so the compiler rebuilds the
     // operands here instead of keeping the prologue's 32 of them (128 VGPRs)
@@ -711,11 +714,14 @@ hadamard128_kernel(const uint16_t *x, uint16_t *y, int64_t rows, float scale) {
 constexpr int kCombineBatch = 16;
 __global__ void __launch_bounds__(256)
 prefill_combine_kernel(const float *__restrict__ part_o, const float *__restrict__ part_ml,
-                       uint16_t *__restrict__ out, int T, int H_q, int n_ksplit) {
+                       uint16_t *__restrict__ out, int T, int H_q, int n_ksplit,
+                       const int32_t *__restrict__ cu_q, int B) {
     __shared__ float obs[4][kD];
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int hq = blockIdx.x * 4 + wave;
     const int t = blockIdx.y;
+    // Rows past the last sequence (a padded q) have no partials: leave them.
+    if (t >= cu_q[B]) return;
     const int64_t split_rows = (int64_t)T * H_q;
     const int64_t row = (int64_t)t * H_q + hq;
     float mi = -INFINITY, li = 0.0f;
@@ -789,7 +795,7 @@ int launch_prefill(const PrefillParams &p, int B, int max_q, hipStream_t st, con
     if (p.n_ksplit > 1) {
         // grid.y = T fits: a split grid has < 256 workgroups, so T < 256 * 64.
         prefill_combine_kernel<<<dim3((unsigned)(p.H_q / 4), (unsigned)p.T_total), 256, 0, st>>>(
-            p.part_o, p.part_ml, p.out, p.T_total, p.H_q, p.n_ksplit);
+            p.part_o, p.part_ml, p.out, p.T_total, p.H_q, p.n_ksplit, p.cu_q, B);
         CDA_LAUNCH_CHECK(std::string(fn) + ": prefill_combine_kernel");
     }
     return CDA_OK;

@@ -21,9 +21,11 @@ def _dev(x, dev):
     return torch.from_numpy(np.ascontiguousarray(x)).to(dev)
 
 
-def run_prefill(case, dev, *, dense=False, scale=None, split=False):
+def run_prefill(case, dev, *, dense=False, scale=None, split=False, max_seq_len=None, pad_rows=0):
     from sub0_amd import _native
     q = _dev(case.q, dev)
+    if pad_rows:
+        q = torch.cat([q, torch.zeros((pad_rows,) + tuple(q.shape[1:]), dtype=q.dtype, device=dev)])
     out = torch.full_like(q, float("nan"))
     cache = _dev(case.cache, dev)
     bt = _dev(case.block_table, dev)
@@ -41,7 +43,7 @@ def run_prefill(case, dev, *, dense=False, scale=None, split=False):
     else:
         _native.prefill_paged(q, cache, bt, cu, sk, cb, cb, out, block_size=case.block_size,
                               max_query_len=max_q, scale=sc,
-                              max_seq_len=max_k if split else None)
+                              max_seq_len=(max_seq_len or max_k) if split else None)
     torch.cuda.synchronize()
     return out.cpu().numpy()
 
@@ -211,3 +213,28 @@ def test_prefill_key_split_negative_scale(gpu):
     case = make_prefill_case(4800, [12], [2500], H_kv=8, gs=4, scale=-0.15)
     out = run_prefill(case, gpu, scale=-0.15, split=True)
     check(out, case.expected)
+
+
+@pytest.mark.parametrize("bound", ["larger", "smaller"])
+def test_prefill_key_split_max_seq_len_bound(gpu, bound):
+    """The split plan follows max_seq_len: a bound above every key length only
+    adds empty splits, one below some length still covers every key (the last
+    split runs to the end of the sequence)."""
+    from sub0_amd import _native
+    print(f"[prefill-split] max_seq_len {bound}", flush=True)
+    case = make_prefill_case(4900, [16, 9], [3000, 1800], H_kv=8, gs=4)
+    msl = 5000 if bound == "larger" else 1200
+    T = int(case.cu_q[-1])
+    assert _native.prefill_workspace_size(2, T, 32, 8, 16, msl) > 0
+    out = run_prefill(case, gpu, split=True, max_seq_len=msl)
+    check(out, case.expected)
+
+
+def test_prefill_key_split_padded_query_rows(gpu):
+    """q padded with rows past cu_seqlens_q[B]: the split path merges only the
+    real rows and leaves the padding rows of out untouched (NaN here)."""
+    print("[prefill-split] padded q rows", flush=True)
+    case = make_prefill_case(4950, [12], [2500], H_kv=8, gs=4)
+    out = run_prefill(case, gpu, split=True, pad_rows=5)
+    check(out[:12], case.expected)
+    assert np.isnan(out[12:]).all()
