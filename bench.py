@@ -453,30 +453,38 @@ def make_encode_workload(dev, levels: int, seed: int = 0xCDA2, n_seq: int = 64,
                 levels=levels, new=new.tolist())
 
 
-def encode_cpu_baseline(levels: int, tokens: int = 2048, reps: int = 3):
-    """The C restatement (oracle/) encoding `tokens` x 8 heads of K and V."""
+def encode_cpu_baseline(levels: int, tokens: int = 2048, reps: int = 5):
+    """The reference's torch CPU encode (oracle/torch_ref.py, the ops of
+    compression.py:315-335) on `tokens` x 8 heads of K and V, all host
+    threads, median of `reps`.  16 levels only (the K4V4 figure)."""
     sys.path.insert(0, str(ROOT))
     import numpy as np
-    from oracle import cda_oracle as O
+    import torch
     from oracle import synth
-    key = "lloyd_beta16" if levels == 16 else "lloyd_beta4"
-    cb = np.load(ROOT / "tests" / "golden" / "codebooks.npz")[key]
-    k = synth.kv_with_outliers(0xCDA2, (tokens, H_KV, D))
-    v = synth.normal_f16(0xCDA3, (tokens, H_KV, D))
-    nt = min(16, os.cpu_count() or 1)
-    O.set_threads(nt)
+    from oracle import torch_ref as TR
+    assert levels == 16
+    cb = torch.from_numpy(np.load(ROOT / "tests" / "golden" / "codebooks.npz")["lloyd_beta16"])
+    k = torch.from_numpy(synth.kv_with_outliers(0xCDA2, (tokens, H_KV, D)))
+    v = torch.from_numpy(synth.normal_f16(0xCDA3, (tokens, H_KV, D)))
+    H = TR.hadamard()
+    nt = os.cpu_count() or 1
+    prev = torch.get_num_threads()
+    torch.set_num_threads(nt)
     ts = []
     for _ in range(reps):
         t0 = time.perf_counter()
-        O.encode(k, cb)
-        O.encode(v, cb)
+        TR.encode(k, cb, H)
+        TR.encode(v, cb, H)
         ts.append(time.perf_counter() - t0)
+    torch.set_num_threads(prev)
     sec = statistics.median(ts)
-    code_bytes = D * (4 if levels == 16 else 2) // 8
+    code_bytes = D * 4 // 8
     nbytes = tokens * (H_KV * D * 2 * 2 + H_KV * (2 * code_bytes + 8) + 4)
     return {"value": round(nbytes / sec / 1e9, 4), "unit": "GB/s", "cores": nt, "kind": "port",
+            "cpu_model": _cpu_model(),
             "sample": f"{tokens} tokens x 8 KV heads, K and V, {sec * 1e3:.1f} ms on {nt} threads "
-                      f"(median of {reps}); the C restatement of Compressor.encode"}
+                      f"(median of {reps}); the reference's torch CPU encode "
+                      f"(oracle/torch_ref.py)"}
 
 
 def encode_main(args) -> int:
@@ -845,53 +853,101 @@ def split_kernel_us(fn, iters: int) -> float:
 
 # ------------------------------------------------------------ cpu baseline --
 
-def cpu_baseline(threads: int | None = None, reps: int = 3):
-    """The C restatement (oracle/) on config 0: B=1, 32/8 heads, N=4096."""
+def _cpu_model() -> str:
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.lower().startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_baseline(threads: int | None = None, reps: int = 5):
+    """The reference's CPU algorithm path on config 0 (B=1, 32/8 heads,
+    N=4096, outliers): ``oracle/torch_ref.py`` restates compression.py's
+    encode and attention.py's attention_compressed with the same torch ops in
+    the same order (bit-identical to the reference's fixtures).  One layer =
+    encode K and V, then one decode step.  Timed with all host threads and
+    with one, median of ``reps``; the C checker (oracle/cda_oracle.c, float64
+    attention) is reported beside it as a second, labelled figure."""
     sys.path.insert(0, str(ROOT))
     import numpy as np
     from oracle import cda_oracle as O
     from oracle import synth
+    from oracle import torch_ref as TR
+    import torch
 
     B, N = 1, 4096
     seed = synth.cfg_seed(B, N)
-    k = synth.kv_with_outliers(seed, (B, H_KV, N, D))
-    v = synth.normal_f16(seed + 1, (B, H_KV, N, D))
-    q = synth.normal_f16(seed + 2, (B, H_Q, D))
-    cb = np.load(ROOT / "tests" / "golden" / "codebooks.npz")["lloyd_beta16"]
-    R = O.hadamard128()
-    bt = synth.permuted_block_table(seed, B, N // BS)
-    res = {}
+    k_np = synth.kv_with_outliers(seed, (B, H_KV, N, D))
+    v_np = synth.normal_f16(seed + 1, (B, H_KV, N, D))
+    q_np = synth.normal_f16(seed + 2, (B, H_Q, 1, D))
+    cb_np = np.load(ROOT / "tests" / "golden" / "codebooks.npz")["lloyd_beta16"]
+    k, v, q = torch.from_numpy(k_np), torch.from_numpy(v_np), torch.from_numpy(q_np)
+    cb = torch.from_numpy(cb_np)
+    H = TR.hadamard()
     ncpu = os.cpu_count() or 1
-    for nt in sorted({1, threads or min(16, ncpu)}):
-        O.set_threads(nt)
+    nt_all = threads or ncpu
+    prev = torch.get_num_threads()
+    res = {}
+    for nt in sorted({1, nt_all}, reverse=True):
+        torch.set_num_threads(nt)
         enc, dec = [], []
         for _ in range(reps):
             t0 = time.perf_counter()
-            kp, kn, _ = O.encode(k, cb)
-            vp, vn, _ = O.encode(v, cb)
+            kc, kn = TR.encode(k, cb, H)
+            vc, vn = TR.encode(v, cb, H)
             t1 = time.perf_counter()
-            cache = O.build_paged_cache(kp, kn, vp, vn, bt, BS, 16)
+            TR.attention_compressed(q, kc, kn, vc, vn, cb, H, H_Q // H_KV)
             t2 = time.perf_counter()
-            O.decode_paged(q, cache, bt, np.full(B, N, np.int32), cb, cb, R, H_kv=H_KV,
-                           block_size=BS)
-            t3 = time.perf_counter()
             enc.append(t1 - t0)
-            dec.append(t3 - t2)
+            dec.append(t2 - t1)
         res[nt] = (statistics.median(enc), statistics.median(dec))
+    torch.set_num_threads(prev)
+    # The C checker, same workload, its OpenMP threads capped at the host's.
+    R = O.hadamard128()
+    bt = synth.permuted_block_table(seed, B, N // BS)
+    O.set_threads(nt_all)
+    c_enc, c_dec = [], []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        kp, kn2, _ = O.encode(k_np, cb_np)
+        vp, vn2, _ = O.encode(v_np, cb_np)
+        t1 = time.perf_counter()
+        cache = O.build_paged_cache(kp, kn2, vp, vn2, bt, BS, 16)
+        t2 = time.perf_counter()
+        O.decode_paged(q_np[:, :, 0], cache, bt, np.full(B, N, np.int32), cb_np, cb_np, R,
+                       H_kv=H_KV, block_size=BS)
+        t3 = time.perf_counter()
+        c_enc.append(t1 - t0)
+        c_dec.append(t3 - t2)
     from sub0_amd._native import decode_algorithmic_bytes
     nbytes = decode_algorithmic_bytes(B, N)
-    nt_max = max(res)
-    enc_s, dec_s = res[nt_max]
+    enc_s, dec_s = res[nt_all]
     return {
         "value": round(nbytes / dec_s / 1e9, 4),
         "unit": "GB/s",
-        "cores": nt_max,
+        "cores": nt_all,
         "kind": "port",
-        "sample": (f"config 0 (B=1, 32/8 heads, N=4096, outliers): decode step "
-                   f"{dec_s * 1e6:.0f} us ({nbytes / 1e6:.2f} MB algorithmic), encode K+V "
-                   f"{enc_s * 1e3:.1f} ms on {nt_max} threads; 1 thread: decode "
-                   f"{res[1][1] * 1e6:.0f} us, encode {res[1][0] * 1e3:.1f} ms; median of "
-                   f"{reps}; host {os.cpu_count()} logical CPUs"),
+        "cpu_model": _cpu_model(),
+        "nproc": ncpu,
+        "us_per_step": round(dec_s * 1e6, 1),
+        "us_per_step_1_thread": round(res[1][1] * 1e6, 1),
+        "sample": (f"config 0, one layer (B=1, 32/8 heads, N=4096, outliers) through the "
+                   f"reference's torch CPU path (oracle/torch_ref.py: compression.py encode + "
+                   f"attention.py attention_compressed, bit-identical to the reference's "
+                   f"fixtures): decode step {dec_s * 1e6:.0f} us ({nbytes / 1e6:.2f} MB "
+                   f"algorithmic), encode K+V {enc_s * 1e3:.1f} ms on {nt_all} threads; "
+                   f"1 thread: decode {res[1][1] * 1e6:.0f} us, encode {res[1][0] * 1e3:.1f} ms; "
+                   f"median of {reps}"),
+        "c_checker": {
+            "value": round(nbytes / statistics.median(c_dec) / 1e9, 4), "unit": "GB/s",
+            "cores": nt_all,
+            "sample": (f"oracle/cda_oracle.c (float64 attention), same workload: decode step "
+                       f"{statistics.median(c_dec) * 1e6:.0f} us, encode K+V "
+                       f"{statistics.median(c_enc) * 1e3:.1f} ms, median of 3"),
+        },
     }
 
 
