@@ -193,6 +193,31 @@ int cda_fa2_varlen_fwd_hadamard(const void *q, const void *k_rot, const void *v_
                                 const int32_t *seqused_k, int B, int T, int H_q, int H_kv,
                                 int max_query_len, int max_seq_len, float scale, void *stream);
 
+/* Comparator kernels behind the FA2-fork torch.ops namespace
+ * (torch.ops._cda_vllm_fa2_fork_C, cda/kernels_vllm_fa2_fork/interface.py:
+ * 138-162, 234-257, 304-328, 434-461); they carry no Hadamard rotation, all
+ * tensors are in one frame.
+ *
+ * cda_fa2_varlen_fwd: the flash attention of cda_fa2_varlen_fwd_hadamard
+ * without the prologue/epilogue rotation, causal (bottom-right) or not
+ * (causal = 0: every key of the sequence visible).  Dense fp16 K/V rows. */
+int cda_fa2_varlen_fwd(const void *q, const void *k, const void *v, void *out,
+                       const int32_t *cu_seqlens_q, const int32_t *cu_seqlens_k,
+                       const int32_t *seqused_k, int B, int T, int H_q, int H_kv,
+                       int max_query_len, float scale, int causal, void *stream);
+
+/* cda_dequantize_rows: out row r = fp16(cb[code] * norm) (compression.py:
+ * 337-361, rotated frame) of code rows (rows, H, 64 or 32 bytes) and norms
+ * (rows, H) fp32 -- the reference fork's dequantize_compressed_kv for one of
+ * K or V.  With block_table != NULL the codes/norms are a paged pool and
+ * out is (B * max_seq_len, H, 128): row b*max_seq_len + t = token t of
+ * sequence b (slot block_table[b][t / block_size] * block_size +
+ * t % block_size), zeros past seq_lens[b]; rows must equal B * max_seq_len. */
+int cda_dequantize_rows(const void *codes, const float *norms, int64_t rows, int H,
+                        const float *cb, int levels, const int32_t *block_table, int bt_stride,
+                        const int32_t *seq_lens, int block_size, int max_seq_len, void *out,
+                        void *stream);
+
 /* Replaces the reference pybind function
  *   cda_fa2_paged_cache_to_dense_rotated(kv, block_table, seq_lens, cb_K, cb_V,
  *                                        block_size, max_seq_len) -> (k_rot, v_rot)

@@ -36,6 +36,8 @@ SYMBOLS = (
     "cda_prefill_workspace_size",
     "cda_prefill_paged_hadamard_ws",
     "cda_fa2_varlen_fwd_hadamard",
+    "cda_fa2_varlen_fwd",
+    "cda_dequantize_rows",
     "cda_fa2_paged_cache_to_dense_rotated",
     "cda_hadamard128_fp16",
 )
@@ -111,6 +113,12 @@ def lib():
         L.cda_fa2_varlen_fwd_hadamard.restype = _I32
         L.cda_fa2_varlen_fwd_hadamard.argtypes = [
             _P, _P, _P, _P, _P, _P, _P, _I32, _I32, _I32, _I32, _I32, _I32, _F32, _P]
+        L.cda_fa2_varlen_fwd.restype = _I32
+        L.cda_fa2_varlen_fwd.argtypes = [
+            _P, _P, _P, _P, _P, _P, _P, _I32, _I32, _I32, _I32, _I32, _F32, _I32, _P]
+        L.cda_dequantize_rows.restype = _I32
+        L.cda_dequantize_rows.argtypes = [
+            _P, _P, _I64, _I32, _P, _I32, _P, _I32, _P, _I32, _I32, _P, _P]
         L.cda_fa2_paged_cache_to_dense_rotated.restype = _I32
         L.cda_fa2_paged_cache_to_dense_rotated.argtypes = [
             _P, _I64, _I32, _I32, _P, _I32, _P, _I32, _P, _P, _I32, _I32, _I32, _P, _P, _P]
@@ -395,6 +403,75 @@ def fa2_varlen_fwd_hadamard(q: torch.Tensor, k_rot: torch.Tensor, v_rot: torch.T
         _ptr(cu_seqlens_k), _ptr(seqused_k), B, T, H_q, k_rot.shape[1], int(max_query_len),
         int(max_seq_len), float(scale), _stream(dev))
     _check(rc, "cda_fa2_varlen_fwd_hadamard")
+
+
+def fa2_varlen_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, out: torch.Tensor,
+                   cu_seqlens_q: torch.Tensor, cu_seqlens_k: torch.Tensor,
+                   seqused_k: torch.Tensor, max_query_len: int, scale: float,
+                   causal: bool) -> None:
+    """Varlen flash attention over dense fp16 K/V rows with no rotation: q, k,
+    v and out all in one frame (the FA2 varlen forward the fork's
+    comparator ops run).  Sequence b's keys are rows cu_seqlens_k[b] ..
+    cu_seqlens_k[b] + seqused_k[b] - 1; causal = bottom-right aligned."""
+    dev = _require_gpu(q, k, v, out, cu_seqlens_q, cu_seqlens_k, seqused_k)
+    for t, nm in ((q, "q"), (k, "k"), (v, "v"), (out, "out")):
+        if t.dtype != torch.float16:
+            raise TypeError(f"{nm} must be fp16")
+        if t.dim() != 3 or t.shape[-1] != 128 or not t.is_contiguous():
+            raise ValueError(f"{nm} must be a contiguous (rows, heads, 128) tensor")
+    if k.shape != v.shape or out.shape != q.shape:
+        raise ValueError("k/v and q/out must have matching shapes")
+    for t, nm in ((cu_seqlens_q, "cu_seqlens_q"), (cu_seqlens_k, "cu_seqlens_k"),
+                  (seqused_k, "seqused_k")):
+        if t.dtype != torch.int32:
+            raise TypeError(f"{nm} must be int32")
+    T, H_q, _ = q.shape
+    B = cu_seqlens_q.numel() - 1
+    rc = lib().cda_fa2_varlen_fwd(
+        _ptr(q), _ptr(k), _ptr(v), _ptr(out), _ptr(cu_seqlens_q), _ptr(cu_seqlens_k),
+        _ptr(seqused_k), B, T, H_q, k.shape[1], int(max_query_len), float(scale),
+        int(bool(causal)), _stream(dev))
+    _check(rc, "cda_fa2_varlen_fwd")
+
+
+def dequantize_rows(codes: torch.Tensor, norms: torch.Tensor, cb: torch.Tensor, *,
+                    block_table: torch.Tensor | None = None,
+                    seq_lens: torch.Tensor | None = None, block_size: int = 0,
+                    max_seq_len: int = 0) -> torch.Tensor:
+    """fp16(cb[code] * norm) rows (compression.py:337-361, rotated frame).
+
+    codes (rows, H, 64 or 32) uint8, norms (rows, H) fp32 -> (rows, H, 128)
+    fp16.  With a block table, codes/norms are a paged pool
+    (num_blocks * block_size rows) and the result is (B * max_seq_len, H,
+    128): sequence b's token t at row b * max_seq_len + t, zeros past
+    seq_lens[b]."""
+    dev = _require_gpu(codes, norms, cb)
+    if codes.dtype != torch.uint8 or norms.dtype != torch.float32 or cb.dtype != torch.float32:
+        raise TypeError("codes must be uint8, norms and cb fp32")
+    codes = codes.contiguous()
+    norms = norms.contiguous()
+    H = codes.shape[-2]
+    levels = cb.numel()
+    if codes.shape[-1] != (64 if levels == 16 else 32):
+        raise ValueError("codes must hold 64 (16 levels) or 32 (4 levels) bytes per row")
+    if block_table is None:
+        rows = codes.numel() // (H * codes.shape[-1])
+        out = torch.empty(rows, H, 128, dtype=torch.float16, device=dev)
+        rc = lib().cda_dequantize_rows(_ptr(codes), _ptr(norms), rows, H,
+                                       _ptr(cb.contiguous()), levels, None, 0, None, 0, 0,
+                                       _ptr(out), _stream(dev))
+    else:
+        if block_table.dtype != torch.int32 or seq_lens is None or seq_lens.dtype != torch.int32:
+            raise TypeError("block_table and seq_lens must be int32")
+        B = seq_lens.numel()
+        rows = B * int(max_seq_len)
+        out = torch.empty(rows, H, 128, dtype=torch.float16, device=dev)
+        rc = lib().cda_dequantize_rows(_ptr(codes), _ptr(norms), rows, H,
+                                       _ptr(cb.contiguous()), levels, _ptr(block_table),
+                                       block_table.stride(0), _ptr(seq_lens), int(block_size),
+                                       int(max_seq_len), _ptr(out), _stream(dev))
+    _check(rc, "cda_dequantize_rows")
+    return out
 
 
 def paged_to_dense(kv_cache: torch.Tensor, block_table: torch.Tensor, seq_lens: torch.Tensor,

@@ -4,9 +4,11 @@ The reference resolves each logical kernel name to a prebuilt CUDA ``.so``
 (``cda/_prebuilt_loader.py:56-80``).  Here every name resolves to one HIP
 library, ``sub0_amd/_lib/libcda_hip.so``, reached through its C ABI.
 ``load_pybind_module(name)`` returns a module object whose attributes have
-the reference's positional signatures; ``load_torch_ops_library(name)``
-mirrors the TORCH_LIBRARY flavour.  Both are ``lru_cache``d and idempotent,
-and raise :class:`PrebuiltMissing` (an ``ImportError``) when the artefact is
+the reference's positional signatures and call the ``torch.ops.cda_hip``
+ops; ``load_torch_ops_library(name)`` returns the registered torch.ops
+namespace (``cda_hip``, or the FA2-fork comparator namespace
+``_cda_vllm_fa2_fork_C``; see :mod:`sub0_amd.cda._torch_ops`).  Both are
+``lru_cache``d and idempotent, and raise :class:`PrebuiltMissing` (an ``ImportError``) when the artefact is
 missing or the name is not provided, as the reference does
 (``_prebuilt_loader.py:41-53``).
 """
@@ -57,11 +59,11 @@ def _make_decode_module(name: str, gs: int) -> ModuleType:
         """Positional signature of the reference call (wrappers.py:115-124)."""
         if int(group_size) != gs:
             raise ValueError(f"{name} is built for group_size={gs}, got {group_size}")
-        _native.decode(Q, _flat_cache(kv_cache), block_table, seq_lens, cb_K, cb_V,
-                       rotation_fp32, rotation_fp16, out, group_size=gs,
-                       block_size=int(block_size), tile_n=int(tile_N),
-                       max_seq_len=int(max_seq_len),
-                       scale=float(scale) if scale is not None else 1.0 / math.sqrt(Q.shape[-1]))
+        torch.ops.cda_hip.decode(
+            Q, _flat_cache(kv_cache), block_table, seq_lens, cb_K, cb_V, rotation_fp32,
+            rotation_fp16 if rotation_fp16 is not None else rotation_fp32, out, gs,
+            int(block_size), int(tile_N), int(max_seq_len),
+            float(scale) if scale is not None else 1.0 / math.sqrt(Q.shape[-1]))
 
     mod.cda_decode_full_hmma_v3 = cda_decode_full_hmma_v3
     return mod
@@ -73,10 +75,14 @@ def _make_encode_module(name: str) -> ModuleType:
 
     def cda_paged_encode_fused(K, V, slot_mapping, flat_cache, cb_K, cb_V):
         """Positional signature of the reference call (wrappers.py:153-156)."""
-        _native.paged_encode(K, V, slot_mapping, _flat_cache(flat_cache), cb_K, cb_V)
+        torch.ops.cda_hip.encode(K, V, slot_mapping, _flat_cache(flat_cache), cb_K, cb_V)
 
     mod.cda_paged_encode_fused = cda_paged_encode_fused
     return mod
+
+
+def _register_ops():
+    from sub0_amd.cda import _torch_ops  # noqa: F401  -- registers torch.ops.cda_hip
 
 
 def _factories():
@@ -100,6 +106,7 @@ def load_pybind_module(name: str) -> ModuleType:
             f"Kernel module '{name}' is not provided by the MI355X build "
             f"(available: {sorted(_factories())}).")
     _lib_or_raise()
+    _register_ops()
     module = fac()
     sys.modules[name] = module
     return module
@@ -107,10 +114,12 @@ def load_pybind_module(name: str) -> ModuleType:
 
 @lru_cache(maxsize=64)
 def load_torch_ops_library(name: str):
-    """TORCH_LIBRARY flavour (reference ``_prebuilt_loader.py:69-80``)."""
-    try:
-        from sub0_amd.cda.kernels_vllm_fa2_fork import _ops
-    except ImportError as e:
-        raise PrebuiltMissing(f"torch.ops library '{name}' is not provided: {e}") from e
+    """TORCH_LIBRARY flavour (reference ``_prebuilt_loader.py:69-80``): the
+    torch.ops namespace ``name`` once its ops are registered."""
+    from sub0_amd.cda import _torch_ops
+    if name not in _torch_ops.NAMESPACES:
+        raise PrebuiltMissing(
+            f"torch.ops library '{name}' is not provided by the MI355X build "
+            f"(available: {list(_torch_ops.NAMESPACES)}).")
     _lib_or_raise()
-    return _ops.namespace(name)
+    return getattr(torch.ops, name)

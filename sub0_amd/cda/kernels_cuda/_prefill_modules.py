@@ -1,13 +1,13 @@
 """Module objects for the prefill kernel names of the reference loader
 (``hmma_loader.py:45-58``): the paged -> dense rotated loader, the fused
 varlen forward with the Hadamard prologue/epilogue, and the Hadamard-128
-helper.  Each forwards to the MI355X C ABI through :mod:`sub0_amd._native`.
+helper.  Each calls the ``torch.ops.cda_hip`` op that wraps the MI355X C ABI.
 """
 from __future__ import annotations
 
 from types import ModuleType
 
-from sub0_amd import _native
+import torch
 
 
 def _flat_cache(kv_cache):
@@ -24,8 +24,8 @@ def _loader_module(name: str) -> ModuleType:
     def cda_fa2_paged_cache_to_dense_rotated(kv_cache, block_table, seq_lens, cb_K, cb_V,
                                              block_size, max_seq_len):
         """Positional signature of the reference call (fa2_cda.py:85-95)."""
-        return _native.paged_to_dense(_flat_cache(kv_cache), block_table, seq_lens, cb_K, cb_V,
-                                      block_size=int(block_size), max_seq_len=int(max_seq_len))
+        return torch.ops.cda_hip.paged_to_dense(_flat_cache(kv_cache), block_table, seq_lens,
+                                                cb_K, cb_V, int(block_size), int(max_seq_len))
 
     mod.cda_fa2_paged_cache_to_dense_rotated = cda_fa2_paged_cache_to_dense_rotated
     return mod
@@ -38,8 +38,8 @@ def _varlen_module(name: str) -> ModuleType:
     def cda_fa2_varlen_fwd_hadamard(Q, k_rot, v_rot, out, cu_q, cu_k, seqused_k, max_q, max_k,
                                     scale):
         """Positional signature of the reference call (fa2_cda.py:166-181)."""
-        _native.fa2_varlen_fwd_hadamard(Q, k_rot, v_rot, out, cu_q, cu_k, seqused_k,
-                                        int(max_q), int(max_k), float(scale))
+        torch.ops.cda_hip.varlen_fwd_hadamard(Q, k_rot, v_rot, out, cu_q, cu_k, seqused_k,
+                                              int(max_q), int(max_k), float(scale))
 
     mod.cda_fa2_varlen_fwd_hadamard = cda_fa2_varlen_fwd_hadamard
     return mod
@@ -51,7 +51,7 @@ def _hadamard_module(name: str) -> ModuleType:
 
     def hadamard128_fp16(x, y, scale):
         """Positional signature of the reference call (fa2_cda.py:51-52)."""
-        _native.hadamard128(x, y, float(scale))
+        torch.ops.cda_hip.hadamard128(x, y, float(scale))
 
     mod.hadamard128_fp16 = hadamard128_fp16
     return mod

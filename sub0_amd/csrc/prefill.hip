@@ -108,6 +108,17 @@ __device__ __forceinline__ half8 hadamard_operand(uint4 hbase, int S, int u, int
     return __builtin_bit_cast(half8, make_uint4(hbase.x ^ f, hbase.y ^ f, hbase.z ^ f, hbase.w ^ f));
 }
 
+// The identity in the same operand layout (row 32T + c32, k = 16S + 8u + e):
+// the prologue and epilogue then copy q and O exactly (one product each).
+__device__ __forceinline__ half8 identity_operand(int S, int u, int T, int c32) {
+    const int e = 32 * T + c32 - 16 * S - 8 * u;
+    uint32_t w[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+        w[i] = (e == 2 * i ? 0x3C00u : 0u) | (e == 2 * i + 1 ? 0x3C000000u : 0u);
+    return __builtin_bit_cast(half8, make_uint4(w[0], w[1], w[2], w[3]));
+}
+
 __device__ __forceinline__ uint4 hadamard_base(int c32) {
     uint32_t w[4];
 #pragma unroll
@@ -159,6 +170,9 @@ struct PrefillParams {
     int n_ksplit;               // 1 = no split
     int ksplit_tiles;
     int T_total;                // rows of q / out
+    int rotate;                 // 1: q and out unrotated (Hadamard prologue/epilogue);
+                                // 0: q and out already in the rotated frame
+    int causal;                 // 1: bottom-right causal mask; 0: every key visible
     float *part_o;              // (n_ksplit, T, H_q, 128) fp32
     float *part_ml;             // (n_ksplit, T, H_q, 2): m (log2 domain), l
 };
@@ -359,7 +373,8 @@ prefill_kernel(PrefillParams p) {
     // was measured 30-40 % slower (the L2 working set grows).
     const int q0 = (int)((KSPLIT ? gridDim.x / p.n_ksplit : gridDim.x) - 1 - lx) * QB;
     if (q0 >= seq_q) return;
-    const int off = seq_k - seq_q;                   // bottom-right causal alignment
+    // Bottom-right causal alignment; without the mask every key is visible.
+    const int off = p.causal ? seq_k - seq_q : seq_k;
     const int q_last = min(q0 + QB, seq_q) - 1;
     const int kend = max(0, min(seq_k, q_last + off + 1));
 
@@ -385,7 +400,8 @@ prefill_kernel(PrefillParams p) {
 
     // ---- prologue: q_rot = fp16(q H / sqrt(128)) (compression.py:290-291) as
     // the B operand of S^T = K q_rot^T, natural k (dims 16S + 8u + 0..7).
-    const float hs = 0.08838834764831845f;          // 1/sqrt(128)
+    const bool rot = p.rotate != 0;
+    const float hs = rot ? 0.08838834764831845f : 1.0f;   // 1/sqrt(128)
     const uint4 hbase = hadamard_base(c32);
     half8 qb[8];
     {
@@ -400,7 +416,8 @@ prefill_kernel(PrefillParams p) {
             floatx16 acc = {};
 #pragma unroll
             for (int S = 0; S < 8; ++S)
-                acc = mfma32(hadamard_operand(hbase, S, u, T, c32), qin[S], acc);
+                acc = mfma32(rot ? hadamard_operand(hbase, S, u, T, c32)
+                                 : identity_operand(S, u, T, c32), qin[S], acc);
             qb[2 * T] = acc_to_operand(acc, 0, u, hs);
             qb[2 * T + 1] = acc_to_operand(acc, 1, u, hs);
         }
@@ -593,7 +610,9 @@ prefill_kernel(PrefillParams p) {
     for (int T = 0; T < 4; ++T) {
         floatx16 acc = {};
 #pragma unroll
-        for (int S = 0; S < 8; ++S) acc = mfma32(hadamard_operand(hb2, S, u, T, c32), ob[S], acc);
+        for (int S = 0; S < 8; ++S)
+            acc = mfma32(rot ? hadamard_operand(hb2, S, u, T, c32)
+                             : identity_operand(S, u, T, c32), ob[S], acc);
         if (store) {
 #pragma unroll
             for (int gi = 0; gi < 4; ++gi) {
@@ -882,6 +901,9 @@ int prefill_paged_impl(const char *fn, const void *q, const void *kv_cache, int 
     p.cb_v = cb_v;
     p.n_ksplit = 1;
     p.T_total = T;
+    p.rotate = 1;
+    p.causal = 1;
+    CDA_REQUIRE(T > 0 || max_query_len == 0, std::string(fn) + ": T must be the number of query rows");
     if (max_seq_len >= 0) {
         int ns, per;
         prefill_ksplit_plan(B, H_q, H_kv, max_query_len, max_seq_len, &ns, &per);
@@ -945,24 +967,27 @@ extern "C" int cda_prefill_paged_hadamard_ws(const void *q, const void *kv_cache
                               workspace_bytes, stream);
 }
 
-extern "C" int cda_fa2_varlen_fwd_hadamard(const void *q, const void *k_rot, const void *v_rot,
-                                           void *out, const int32_t *cu_seqlens_q,
-                                           const int32_t *cu_seqlens_k, const int32_t *seqused_k,
-                                           int B, int T, int H_q, int H_kv, int max_query_len,
-                                           int max_seq_len, float scale, void *stream) {
-    const char *fn = "cda_fa2_varlen_fwd_hadamard";
-    (void)T;
-    (void)max_seq_len;
-    CDA_REQUIRE(q && k_rot && v_rot && out && cu_seqlens_q && cu_seqlens_k && seqused_k,
-                "cda_fa2_varlen_fwd_hadamard: null pointer argument");
+namespace cda {
+namespace {
+// Causal / non-causal varlen flash attention over dense fp16 K/V rows, with
+// (rotate = 1) or without the Hadamard prologue and epilogue.
+int fa2_varlen_dense(const void *q, const void *k, const void *v, void *out,
+                     const int32_t *cu_seqlens_q, const int32_t *cu_seqlens_k,
+                     const int32_t *seqused_k, int B, int T, int H_q, int H_kv,
+                     int max_query_len, float scale, int causal, int rotate, void *stream,
+                     const char *fn) {
+    const std::string f(fn);
+    CDA_REQUIRE(q && k && v && out && cu_seqlens_q && cu_seqlens_k && seqused_k,
+                f + ": null pointer argument");
     CDA_REQUIRE(B >= 0 && H_kv > 0 && H_q > 0 && max_query_len >= 0,
-                "cda_fa2_varlen_fwd_hadamard: bad B / H_q / H_kv / max_query_len");
+                f + ": bad B / H_q / H_kv / max_query_len");
     CDA_REQUIRE(H_q % H_kv == 0 && (H_q / H_kv == 4 || H_q / H_kv == 8),
-                "cda_fa2_varlen_fwd_hadamard: H_q / H_kv must be 4 or 8");
+                f + ": H_q / H_kv must be 4 or 8");
     CDA_REQUIRE(((uintptr_t)q & 15) == 0 && ((uintptr_t)out & 15) == 0 &&
-                    ((uintptr_t)k_rot & 15) == 0 && ((uintptr_t)v_rot & 15) == 0,
-                "cda_fa2_varlen_fwd_hadamard: tensors must be 16-byte aligned");
+                    ((uintptr_t)k & 15) == 0 && ((uintptr_t)v & 15) == 0,
+                f + ": tensors must be 16-byte aligned");
     if (B == 0 || max_query_len == 0) return CDA_OK;
+    CDA_REQUIRE(T > 0, f + ": T must be the number of query rows");
     PrefillParams p{};
     p.q = static_cast<const uint16_t *>(q);
     p.out = static_cast<uint16_t *>(out);
@@ -972,12 +997,122 @@ extern "C" int cda_fa2_varlen_fwd_hadamard(const void *q, const void *k_rot, con
     p.H_kv = H_kv;
     p.GS = H_q / H_kv;
     p.scale_log2 = scale * kLog2e;
-    p.k_rot = static_cast<const uint16_t *>(k_rot);
-    p.v_rot = static_cast<const uint16_t *>(v_rot);
+    p.k_rot = static_cast<const uint16_t *>(k);
+    p.v_rot = static_cast<const uint16_t *>(v);
     p.cu_k = cu_seqlens_k;
     p.n_ksplit = 1;
     p.T_total = T;
+    p.rotate = rotate;
+    p.causal = causal;
     return launch_prefill<false>(p, B, max_query_len, static_cast<hipStream_t>(stream), fn);
+}
+
+// out row r (fp16, 128 dims) = fp16(cb[code] * norm) of source row src(r):
+// src(r) = r, or, with a block table, the slot of token t = r % max_seq of
+// sequence b = r / max_seq (rows past seq_lens[b] are zero).  One thread per
+// (row, 16-dim chunk); codes MSB-first, 4-bit (levels 16) or 2-bit (4).
+__global__ void __launch_bounds__(256)
+dequant_rows_kernel(const uint8_t *codes, const float *norms, int64_t rows, int H,
+                    const float *cb, int levels, const int32_t *block_table, int bt_stride,
+                    const int32_t *seq_lens, int block_size, int max_seq, uint16_t *out) {
+    __shared__ float lut[16];
+    if (threadIdx.x < 16) lut[threadIdx.x] = threadIdx.x < levels ? cb[threadIdx.x] : 0.0f;
+    __syncthreads();
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;   // (row, head, chunk)
+    if (i >= rows * H * 8) return;
+    const int c = (int)(i & 7);
+    const int64_t rh = i >> 3;
+    const int h = (int)(rh % H);
+    const int64_t r = rh / H;
+    int64_t src = r;
+    bool zero = false;
+    if (block_table) {
+        const int64_t b = r / max_seq;
+        const int t = (int)(r - b * max_seq);
+        zero = t >= seq_lens[b];
+        src = zero ? 0 : (int64_t)block_table[b * bt_stride + t / block_size] * block_size +
+                             t % block_size;
+    }
+    uint32_t w[8];
+    if (zero) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) w[j] = 0;
+    } else {
+        const int cbytes = levels == 16 ? 64 : 32;
+        const uint8_t *row = codes + (src * H + h) * cbytes;
+        const float nrm = norms[src * H + h];
+        float x[16];
+        if (levels == 16) {
+            const uint2 cw = *reinterpret_cast<const uint2 *>(row + 8 * c);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const uint32_t byte = ((j < 4 ? cw.x : cw.y) >> (8 * (j & 3))) & 0xFFu;
+                x[2 * j] = lut[byte >> 4];
+                x[2 * j + 1] = lut[byte & 15];
+            }
+        } else {
+            const uint32_t cw = *reinterpret_cast<const uint32_t *>(row + 4 * c);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const uint32_t byte = (cw >> (8 * j)) & 0xFFu;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) x[4 * j + e] = lut[(byte >> (6 - 2 * e)) & 3];
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+            w[j] = (uint32_t)__half_as_ushort(__float2half_rn(x[2 * j] * nrm)) |
+                   ((uint32_t)__half_as_ushort(__float2half_rn(x[2 * j + 1] * nrm)) << 16);
+    }
+    uint4 *dst = reinterpret_cast<uint4 *>(out + (r * H + h) * kD + 16 * c);
+    dst[0] = make_uint4(w[0], w[1], w[2], w[3]);
+    dst[1] = make_uint4(w[4], w[5], w[6], w[7]);
+}
+}  // namespace
+}  // namespace cda
+
+extern "C" int cda_fa2_varlen_fwd_hadamard(const void *q, const void *k_rot, const void *v_rot,
+                                           void *out, const int32_t *cu_seqlens_q,
+                                           const int32_t *cu_seqlens_k, const int32_t *seqused_k,
+                                           int B, int T, int H_q, int H_kv, int max_query_len,
+                                           int max_seq_len, float scale, void *stream) {
+    (void)max_seq_len;
+    return fa2_varlen_dense(q, k_rot, v_rot, out, cu_seqlens_q, cu_seqlens_k, seqused_k, B, T,
+                            H_q, H_kv, max_query_len, scale, 1, 1, stream,
+                            "cda_fa2_varlen_fwd_hadamard");
+}
+
+extern "C" int cda_fa2_varlen_fwd(const void *q, const void *k, const void *v, void *out,
+                                  const int32_t *cu_seqlens_q, const int32_t *cu_seqlens_k,
+                                  const int32_t *seqused_k, int B, int T, int H_q, int H_kv,
+                                  int max_query_len, float scale, int causal, void *stream) {
+    return fa2_varlen_dense(q, k, v, out, cu_seqlens_q, cu_seqlens_k, seqused_k, B, T, H_q, H_kv,
+                            max_query_len, scale, causal != 0, 0, stream, "cda_fa2_varlen_fwd");
+}
+
+extern "C" int cda_dequantize_rows(const void *codes, const float *norms, int64_t rows, int H,
+                                   const float *cb, int levels, const int32_t *block_table,
+                                   int bt_stride, const int32_t *seq_lens, int block_size,
+                                   int max_seq_len, void *out, void *stream) {
+    CDA_REQUIRE(codes && norms && cb && out && rows >= 0 && H > 0,
+                "cda_dequantize_rows: bad arguments");
+    CDA_REQUIRE(levels == 16 || levels == 4, "cda_dequantize_rows: levels must be 16 or 4");
+    CDA_REQUIRE(((uintptr_t)codes & 7) == 0 && ((uintptr_t)out & 15) == 0,
+                "cda_dequantize_rows: codes must be 8-byte and out 16-byte aligned");
+    if (block_table) {
+        CDA_REQUIRE(seq_lens && bt_stride > 0 && block_size > 0 && max_seq_len > 0 &&
+                        rows % max_seq_len == 0,
+                    "cda_dequantize_rows: paged form needs seq_lens, bt_stride, block_size and "
+                    "rows = B * max_seq_len");
+    }
+    if (rows == 0) return CDA_OK;
+    const int64_t threads = rows * H * 8;
+    dequant_rows_kernel<<<(unsigned)((threads + 255) / 256), 256, 0,
+                          static_cast<hipStream_t>(stream)>>>(
+        static_cast<const uint8_t *>(codes), norms, rows, H, cb, levels, block_table, bt_stride,
+        seq_lens, block_size, max_seq_len, static_cast<uint16_t *>(out));
+    CDA_LAUNCH_CHECK("dequant_rows_kernel");
+    return CDA_OK;
 }
 
 extern "C" int cda_fa2_paged_cache_to_dense_rotated(const void *kv_cache, int64_t num_slots,

@@ -78,3 +78,48 @@ def test_prefill_source_policy(monkeypatch):
     monkeypatch.setenv("CDA_PREFILL_SOURCE", "fast")
     with pytest.raises(ValueError):
         prefill_source(8, 8, 7643, 7643)
+
+
+def test_torch_ops_schemas_and_fake_kernels():
+    """Both torch.ops namespaces are registered with in-place annotations on
+    the outputs, load_torch_ops_library returns them, and the fake kernels
+    trace without a GPU."""
+    from sub0_amd.cda._prebuilt_loader import PrebuiltMissing, load_torch_ops_library
+    ns = load_torch_ops_library("cda_hip")
+    assert ns is torch.ops.cda_hip
+    sch = str(torch.ops.cda_hip.decode.default._schema)
+    assert "Tensor(a!) out" in sch and "int group_size" in sch and sch.endswith("-> ()")
+    assert "Tensor(a!) flat_cache" in str(torch.ops.cda_hip.encode.default._schema)
+    assert "Tensor(a!) out" in str(torch.ops.cda_hip.prefill.default._schema)
+    assert "Tensor(a!) y" in str(torch.ops.cda_hip.hadamard128.default._schema)
+    fork = load_torch_ops_library("_cda_vllm_fa2_fork_C")
+    for op in ("dequantize_compressed_kv", "varlen_fwd", "varlen_fwd_compressed_kv",
+               "varlen_fwd_compressed_kv_fused"):
+        assert hasattr(fork, op)
+    fsch = str(fork.varlen_fwd_compressed_kv_fused.default._schema)
+    # the reference's positional order (interface.py:434-461)
+    names = [a.name for a in fork.varlen_fwd_compressed_kv_fused.default._schema.arguments]
+    assert names[:13] == ["q", "k_idx", "k_norm", "v_idx", "v_norm", "cb_k", "cb_v", "out",
+                          "cu_seqlens_q", "cu_seqlens_k", "seqused_k", "block_table",
+                          "alibi_slopes"]
+    assert names[-2:] == ["uniform_codebook", "gen"] and "Tensor[]" in fsch
+    with pytest.raises(PrebuiltMissing):
+        load_torch_ops_library("no_such_namespace")
+    from torch._subclasses.fake_tensor import FakeTensorMode
+    with FakeTensorMode():
+        kv = torch.empty(64, 8, 144, dtype=torch.uint8, device="cuda")
+        bt = torch.empty(2, 4, dtype=torch.int32, device="cuda")
+        sl = torch.empty(2, dtype=torch.int32, device="cuda")
+        cb = torch.empty(16, device="cuda")
+        k, v = torch.ops.cda_hip.paged_to_dense(kv, bt, sl, cb, cb, 16, 40)
+        assert k.shape == (80, 8, 128) and k.dtype == torch.float16
+        ki = torch.empty(100, 8, 64, dtype=torch.uint8, device="cuda")
+        kn = torch.empty(100, 8, device="cuda")
+        kd, vd = fork.dequantize_compressed_kv(ki, kn, ki, kn, cb, cb)
+        assert kd.shape == (100, 8, 128)
+
+
+def test_fa2_fork_build_stub():
+    from sub0_amd.cda.kernels_vllm_fa2_fork import build
+    build.load()
+    assert hasattr(torch.ops._cda_vllm_fa2_fork_C, "varlen_fwd")
