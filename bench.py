@@ -631,12 +631,14 @@ class E2EModel:
 
 
 def e2e_run(dev, *, B=32, prefix=16384, steps=256, layers=32, heads=32, kv_heads=8,
-            ffn=14336, vocab=32000, seed=0xCDA4, check_eager=0):
+            ffn=14336, vocab=32000, seed=0xCDA4, check_eager=0, keep_state=False):
     """Prefill B random prefixes through the model (one request per forward),
     then `steps` greedy decode steps of all B requests as replays of one
     captured step (state advanced inside the graph).  Returns a dict of
     timings; with check_eager > 0 also the tokens of that many eager steps
-    run from the same state, for comparison with the replays."""
+    run from the same state, for comparison with the replays; with
+    keep_state the model, the per-layer caches, the block table and the
+    final sequence lengths (tokens in the cache)."""
     import torch
     m = E2EModel(dev, layers=layers, heads=heads, kv_heads=kv_heads, ffn=ffn, vocab=vocab,
                  seed=seed)
@@ -744,9 +746,14 @@ def e2e_run(dev, *, B=32, prefix=16384, steps=256, layers=32, heads=32, kv_heads
         ga.replay()
     torch.cuda.synchronize()
     attn_s = (time.perf_counter() - t0) / reps
-    return dict(prefill_s=prefill_s, decode_s=decode_s, decode_steps=n,
-                step_ms=decode_s / n * 1e3, attn_ms=attn_s * 1e3,
-                tokens_per_s=B * n / decode_s, produced=produced, eager_tokens=eager_tokens)
+    r = dict(prefill_s=prefill_s, decode_s=decode_s, decode_steps=n,
+             step_ms=decode_s / n * 1e3, attn_ms=attn_s * 1e3,
+             tokens_per_s=B * n / decode_s, produced=produced, eager_tokens=eager_tokens)
+    if keep_state:
+        # the attention-share replays above wrote the next token's slots; the
+        # tokens before it are the model's own
+        r.update(model=m, caches=caches, block_table=bt, cached_lens=(seq - 1).clone())
+    return r
 
 
 def e2e_main(args) -> int:

@@ -29,3 +29,50 @@ def test_e2e_gs8_heads(gpu):
                       vocab=300, check_eager=2)
     for i, want in enumerate(r["eager_tokens"]):
         assert torch.equal(r["produced"][2 + i], want)
+
+
+def test_e2e_config4_full_size(gpu):
+    """BASELINE config 4 at its stated shape: 32 layers, hidden 4096, 32/8
+    heads, SwiGLU 14336, 32 sequences x 16384-token prefix, K4V4 cache, 8
+    greedy steps.  Replayed steps produce the eager steps' tokens, and one
+    layer's decode over its ~16.4K-token cache is within 2e-3 of a float64
+    torch reference on the dense dequantised rows of that cache."""
+    import bench
+    from sub0_amd import _native
+    print("[e2e] config 4: B=32 prefix=16384 steps=8 layers=32", flush=True)
+    r = bench.e2e_run(gpu, B=32, prefix=16384, steps=8, check_eager=3, keep_state=True)
+    for i, want in enumerate(r["eager_tokens"]):
+        assert torch.equal(r["produced"][2 + i], want), f"replay {i + 1}"
+    m, caches, bt = r["model"], r["caches"], r["block_table"]
+    lens = r["cached_lens"].to(torch.int32)
+    N = int(lens[0])
+    assert bool((lens == N).all()) and N == 16384 + 8
+    li = 17
+    A = m.A
+    B, H, Hkv, D = 32, 32, 8, 128
+    g = torch.Generator(device=gpu).manual_seed(5)
+    q = torch.randn(B, H, D, generator=g, device=gpu, dtype=torch.float16)
+    md = A.CDAv2AttentionMetadata(
+        num_actual_tokens=B, num_reqs=B, max_query_len=1, max_seq_len=N,
+        query_start_loc=torch.arange(B + 1, dtype=torch.int32, device=gpu),
+        seq_lens=lens, block_table=bt,
+        slot_mapping=torch.zeros(B, dtype=torch.int64, device=gpu))
+    out = torch.empty(B, H * D, dtype=torch.float16, device=gpu)
+    m.impl.forward(None, q, q[:, :Hkv], q[:, :Hkv], caches[li], md, out)
+    torch.cuda.synchronize()
+    kv = A._as_uint8_cache(caches[li]).reshape(-1, Hkv, 144)
+    cb, _, R, _ = A._get_hmma_artifacts(*A._get_compressors(gpu), gpu)
+    k_rot, v_rot = _native.paged_to_dense(kv, bt, lens, cb, cb, block_size=16, max_seq_len=N)
+    q_rot = (q.double() @ R.double()).float().half().double()
+    ref = torch.empty(B, H, D, dtype=torch.float16, device=gpu)
+    for b in range(B):
+        K = k_rot[b * N:(b + 1) * N].double()
+        V = v_rot[b * N:(b + 1) * N].double()
+        for h in range(Hkv):
+            s = (q_rot[b, 4 * h:4 * h + 4] @ K[:, h].T) / D ** 0.5
+            o_rot = (torch.softmax(s, dim=-1) @ V[:, h]).float().half().double()
+            ref[b, 4 * h:4 * h + 4] = (o_rot @ R.double().T).float().half()
+    err = (out.view(B, H, D).float() - ref.float()).abs().max().item()
+    print(f"[e2e] config 4 layer {li} decode max abs err {err:.3e}", flush=True)
+    assert err <= 2e-3
+
