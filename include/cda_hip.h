@@ -102,8 +102,8 @@ int cda_decode_set_timing_events(void *start_event, void *stop_event);
 
 /* Selects the decode split kernel for later calls (process-wide; default 1).
  * enable=1 lets cda_decode_full_hmma_v3 use the page-streaming kernel when the
- * cache is 8 KV heads x 144-byte (K4V4) or 80-byte (K2V2) slots and cb_k ==
- * cb_v (same pointer);
+ * cache is 8 KV heads x 144-byte (K4V4) or 80-byte (K2V2) slots and the K and
+ * V codebooks hold equal bits (one pointer, or two compared on the device);
  * enable=0 always takes the general kernel.  Both produce the same result to
  * fp32 rounding of the softmax sums.  No reference counterpart: the reference
  * has one decode kernel; this exists for A/B measurement and tests. */

@@ -8,7 +8,6 @@ call raises.
 from __future__ import annotations
 
 import ctypes
-import weakref
 import threading
 from pathlib import Path
 
@@ -169,33 +168,6 @@ def decode_workspace_size(B: int, H_q: int, H_kv: int, max_seq_len: int, tile_n:
     return int(lib().cda_decode_workspace_size(B, H_q, H_kv, max_seq_len, tile_n))
 
 
-_CB_EQUAL: dict = {}
-
-
-def _same_codebook(cb_k: torch.Tensor, cb_v: torch.Tensor) -> bool:
-    """True when cb_k and cb_v hold the same values (then one pointer is
-    passed for both, which lets eligible caches take the page-streaming
-    kernel).  The comparison syncs once per pair of live tensors and version;
-    during graph capture an unseen pair counts as different."""
-    if cb_k.data_ptr() == cb_v.data_ptr():
-        return True
-    key = (id(cb_k), id(cb_v))
-    hit = _CB_EQUAL.get(key)
-    if hit is not None:
-        rk, rv, stamp, equal = hit
-        if rk() is cb_k and rv() is cb_v and stamp == (cb_k._version, cb_v._version,
-                                                         cb_k.data_ptr(), cb_v.data_ptr()):
-            return equal
-    if torch.cuda.is_current_stream_capturing():
-        return False
-    equal = bool(torch.equal(cb_k, cb_v))
-    if len(_CB_EQUAL) > 64:
-        _CB_EQUAL.clear()
-    _CB_EQUAL[key] = (weakref.ref(cb_k), weakref.ref(cb_v),
-                      (cb_k._version, cb_v._version, cb_k.data_ptr(), cb_v.data_ptr()), equal)
-    return equal
-
-
 def decode(q: torch.Tensor, kv_cache: torch.Tensor, block_table: torch.Tensor,
            seq_lens: torch.Tensor, cb_k: torch.Tensor, cb_v: torch.Tensor,
            rot_f32: torch.Tensor, rot_f16: torch.Tensor | None, out: torch.Tensor, *,
@@ -233,7 +205,7 @@ def decode(q: torch.Tensor, kv_cache: torch.Tensor, block_table: torch.Tensor,
     if block_table.shape[0] < B or seq_lens.numel() < B:
         raise ValueError("block_table / seq_lens have fewer rows than q")
     cb_k = cb_k.contiguous()
-    cb_v = cb_k if _same_codebook(cb_k, cb_v) else cb_v.contiguous()
+    cb_v = cb_k if cb_v.data_ptr() == cb_k.data_ptr() else cb_v.contiguous()
     need = decode_workspace_size(B, H_q, H_kv, max_seq_len, tile_n)
     if (workspace is None or workspace.device != dev
             or workspace.numel() - ((-workspace.data_ptr()) % 256) < need):

@@ -68,6 +68,10 @@ struct SplitParams {
     int n_splits;
     float scale_log2;           // softmax scale * log2(e)
     int levels;                 // codebook levels: 16 (4-bit codes) or 4 (2-bit codes)
+    // Set when both split kernels are launched (codebooks passed as two
+    // pointers): 1 if they hold equal bits.  The page-streaming kernel runs
+    // only if 1, the general kernel only if 0.
+    const int *cb_same;
 };
 
 __device__ __forceinline__ floatx4 mfma16(uint4 a, uint4 b, floatx4 c) {
@@ -173,6 +177,7 @@ __device__ __forceinline__ void load_tile(Chunk &c, int t, rsrc_t r, const LaneO
 template <int GS, int L>
 __global__ void __launch_bounds__(kThreads, 1)
 decode_split_kernel(SplitParams p) {
+    if (p.cb_same && *p.cb_same) return;        // the page-streaming kernel covers this call
     __shared__ __align__(16) uint32_t lds[kLutDwords];
 
     const int sp = blockIdx.x;
@@ -537,6 +542,7 @@ __device__ __forceinline__ uint32_t bfi(uint32_t m, uint32_t a, uint32_t b) {
 template <int GS, int L>
 __global__ void __launch_bounds__(kThreads, 1)
 decode_stream_kernel(SplitParams p) {
+    if (p.cb_same && !*p.cb_same) return;       // different codebooks: the general kernel runs
     static_assert(L == 16 || L == 4, "4-bit or 2-bit codes");
     __shared__ __align__(16) uint8_t smem[kStreamLds];
     constexpr int S = (L == 16) ? 144 : 80;        // slot bytes
@@ -927,10 +933,18 @@ decode_stream_kernel(SplitParams p) {
 constexpr int kHeadsPerBlock = 4;
 
 __global__ void __launch_bounds__(256)
-rotate_q_kernel(const uint16_t *q, const float *R, uint16_t *q_rot, int H_q) {
+rotate_q_kernel(const uint16_t *q, const float *R, uint16_t *q_rot, int H_q,
+                const float *cb_k, const float *cb_v, int levels, int *cb_same) {
     __shared__ __align__(16) float Rs[kD * kD];
     __shared__ float qs[kHeadsPerBlock][kD];
     const int b = blockIdx.y, t = threadIdx.x;
+    if (cb_same && blockIdx.x == 0 && blockIdx.y == 0 && t < 64) {
+        // Whether the K and V codebooks hold the same bits: selects between
+        // the two split kernels launched after this one.
+        const bool eq = t >= levels || __float_as_uint(cb_k[t]) == __float_as_uint(cb_v[t]);
+        const bool all = __builtin_amdgcn_ballot_w64(!eq) == 0;
+        if (t == 0) *cb_same = all ? 1 : 0;
+    }
     const int h0 = blockIdx.x * kHeadsPerBlock;
     const float4 *R4 = reinterpret_cast<const float4 *>(R);
     float4 *Rs4 = reinterpret_cast<float4 *>(Rs);
@@ -1120,7 +1134,7 @@ combine_kernel(const float *part_o, const float *part_ml, const float *R, uint16
 }
 
 struct WsLayout {
-    size_t q_rot, part_o, part_ml, total;
+    size_t q_rot, part_o, part_ml, flag, total;
 };
 
 WsLayout ws_layout(int B, int H_q, int n_splits) {
@@ -1132,6 +1146,8 @@ WsLayout ws_layout(int B, int H_q, int n_splits) {
     off += align256((size_t)B * n_splits * H_q * kD * 4);
     w.part_ml = off;
     off += align256((size_t)B * n_splits * H_q * 2 * 4);
+    w.flag = off;
+    off += 256;
     w.total = off;
     return w;
 }
@@ -1247,8 +1263,20 @@ extern "C" int cda_decode_full_hmma_v3(const void *q, const void *kv_cache, int6
 
     uint16_t *q_rot = reinterpret_cast<uint16_t *>(ws + w.q_rot);
     const dim3 head_grid((H_q + kHeadsPerBlock - 1) / kHeadsPerBlock, B);
+    // The page-streaming kernel covers 8 KV heads x 144-byte (K4V4) or
+    // 80-byte (K2V2) slots with one codebook for K and V, and splits of at
+    // most 1024 pages.  With one codebook pointer it runs alone; with two, the
+    // rotation kernel compares them on the device and both split kernels are
+    // launched, each returning at once unless the comparison picks it (no
+    // host round trip, so the choice is the same inside graph capture).
+    const bool stream_shape = H_kv == 8 &&
+                              ((levels == 16 && slot_bytes == 144) ||
+                               (levels == 4 && slot_bytes == 80)) &&
+                              tn <= 16 * kStreamMaxPages && g_allow_stream;
+    const bool dual = stream_shape && cb_k != cb_v;
+    int *cb_same = dual ? reinterpret_cast<int *>(ws + w.flag) : nullptr;
     rotate_q_kernel<<<head_grid, 256, 0, st>>>(static_cast<const uint16_t *>(q), rot_f32, q_rot,
-                                               H_q);
+                                               H_q, cb_k, cb_v, levels, cb_same);
     CDA_LAUNCH_CHECK("rotate_q_kernel");
 
     SplitParams p;
@@ -1270,36 +1298,35 @@ extern "C" int cda_decode_full_hmma_v3(const void *q, const void *kv_cache, int6
     p.n_splits = ns;
     p.scale_log2 = scale * kLog2e;
     p.levels = levels;
+    p.cb_same = cb_same;
     dim3 grid(ns, (H_kv + kWaves - 1) / kWaves, B);
-    // The page-streaming kernel covers 8 KV heads x 144-byte slots with one
-    // codebook for K and V (passed as the same pointer) and splits of at most
-    // 1024 pages; anything else takes the general kernel.
-    const bool use_stream = H_kv == 8 &&
-                            ((levels == 16 && slot_bytes == 144) ||
-                             (levels == 4 && slot_bytes == 80)) &&
-                            cb_k == cb_v &&
-                            tn <= 16 * kStreamMaxPages && g_allow_stream;
+    const bool use_stream = stream_shape;
     if (g_split_start && hipEventRecord(g_split_start, st) != hipSuccess)
         return fail(CDA_E_HIP, "cda_decode_full_hmma_v3: hipEventRecord(start) failed");
-    if (use_stream && levels == 16) {
-        if (group_size == 4)
-            decode_stream_kernel<4, 16><<<grid, kThreads, 0, st>>>(p);
-        else
-            decode_stream_kernel<8, 16><<<grid, kThreads, 0, st>>>(p);
-    } else if (use_stream) {
-        if (group_size == 4)
-            decode_stream_kernel<4, 4><<<grid, kThreads, 0, st>>>(p);
-        else
-            decode_stream_kernel<8, 4><<<grid, kThreads, 0, st>>>(p);
-    } else if (levels == 4) {
-        if (group_size == 4)
-            decode_split_kernel<4, 4><<<grid, kThreads, 0, st>>>(p);
-        else
-            decode_split_kernel<8, 4><<<grid, kThreads, 0, st>>>(p);
-    } else if (group_size == 4) {
-        decode_split_kernel<4, 16><<<grid, kThreads, 0, st>>>(p);
-    } else {
-        decode_split_kernel<8, 16><<<grid, kThreads, 0, st>>>(p);
+    if (use_stream) {
+        if (levels == 16) {
+            if (group_size == 4)
+                decode_stream_kernel<4, 16><<<grid, kThreads, 0, st>>>(p);
+            else
+                decode_stream_kernel<8, 16><<<grid, kThreads, 0, st>>>(p);
+        } else {
+            if (group_size == 4)
+                decode_stream_kernel<4, 4><<<grid, kThreads, 0, st>>>(p);
+            else
+                decode_stream_kernel<8, 4><<<grid, kThreads, 0, st>>>(p);
+        }
+    }
+    if (!use_stream || dual) {
+        if (levels == 4) {
+            if (group_size == 4)
+                decode_split_kernel<4, 4><<<grid, kThreads, 0, st>>>(p);
+            else
+                decode_split_kernel<8, 4><<<grid, kThreads, 0, st>>>(p);
+        } else if (group_size == 4) {
+            decode_split_kernel<4, 16><<<grid, kThreads, 0, st>>>(p);
+        } else {
+            decode_split_kernel<8, 16><<<grid, kThreads, 0, st>>>(p);
+        }
     }
     CDA_LAUNCH_CHECK("decode_split_kernel");
     if (g_split_stop && hipEventRecord(g_split_stop, st) != hipSuccess)

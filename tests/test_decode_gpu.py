@@ -232,3 +232,39 @@ def test_decode_graph_replay(gpu):
         g.replay()
         torch.cuda.synchronize()
         assert torch.equal(out, eager)
+
+
+@pytest.mark.parametrize("same_values", [True, False], ids=["equal_cb", "different_cb"])
+def test_decode_capture_first(gpu, same_values):
+    """Graph capture before any eager call, with K and V codebooks passed as
+    two tensors: the kernel choice is made on the device, so the replays are
+    right for equal and for different codebooks."""
+    from sub0_amd import _native
+    print(f"[decode] capture first, same_values={same_values}", flush=True)
+    cbv_np = None if same_values else O.uniform_centroids(16)
+    case = make_decode_case(3100, [1100, 40, 2500], H_kv=8, gs=4, fill=0xFF, cb_v=cbv_np)
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(gpu)
+    q, cache, bt, sl = t(case.q), t(case.cache), t(case.block_table), t(case.seq_lens)
+    cb = t(case.cb_k)
+    cbv = t(case.cb_v.copy())                       # a distinct tensor in both cases
+    R = t(case.R)
+    out = torch.full_like(q, float("nan"))
+    ws = torch.empty(_native.decode_workspace_size(3, 32, 8, 2500) + 256, dtype=torch.uint8,
+                     device=gpu)
+
+    def call():
+        _native.decode(q, cache, bt, sl, cb, cbv, R, R.half(), out, group_size=4, block_size=16,
+                       tile_n=0, max_seq_len=2500, scale=float(1 / np.sqrt(128)), workspace=ws)
+
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            call()
+    torch.cuda.current_stream().wait_stream(s)
+    for _ in range(3):
+        out.fill_(float("nan"))
+        g.replay()
+        torch.cuda.synchronize()
+        check(out.cpu().numpy(), case.expected)
