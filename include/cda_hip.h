@@ -74,6 +74,20 @@ int cda_decode_full_hmma_v3(const void *q, const void *kv_cache, int64_t num_slo
                             int block_size, int tile_n, int max_seq_len, float scale,
                             void *workspace, size_t workspace_bytes, void *stream);
 
+/* The legacy K4V2 cache (cda_attn_v2.py:29: "legacy K4V2 layout (104 B/slot)"):
+ * slot = [K codes 4-bit 64 B | V codes 2-bit 32 B | K norm fp32 | V norm fp32],
+ * 104 bytes (slot_bytes >= 104, a multiple of 8); cb_k has 16 levels, cb_v 4.
+ * Replaces the module of load_decode_hmma(k4v2=True) (_v1_decode_hmma_k4v2_gs{4,8},
+ * hmma_loader.py:27-32), same arguments as cda_decode_full_hmma_v3 with the
+ * level count implied.  Runs the general split kernel. */
+int cda_decode_full_hmma_v3_k4v2(const void *q, const void *kv_cache, int64_t num_slots,
+                                 int slot_bytes, int H_kv, const int32_t *block_table,
+                                 int bt_stride, const int32_t *seq_lens, const float *cb_k,
+                                 const float *cb_v, const float *rot_f32, const void *rot_f16,
+                                 void *out, int B, int H_q, int group_size, int block_size,
+                                 int tile_n, int max_seq_len, float scale, void *workspace,
+                                 size_t workspace_bytes, void *stream);
+
 /* Allocation-free variant of cda_decode_full_hmma_v3.  No counterpart in the
  * reference: it is for callers that cannot allocate device memory (code
  * under graph capture that must not call hipMalloc, tight serving loops,
@@ -130,6 +144,17 @@ int cda_paged_encode_fused(const void *k, const void *v, int64_t k_stride, int64
                            const int32_t *slot_mapping, int64_t num_tokens, void *flat_cache,
                            int64_t num_slots, int slot_bytes, int H_kv, const float *cb_k,
                            const float *cb_v, int levels, void *stream);
+
+/* cda_paged_encode_fused into the legacy K4V2 slot (104 B, layout above the
+ * K4V2 decode): K with the 16-level cb_k, V with the 4-level cb_v.  Replaces
+ * the K4V2 cache-update module (_v1_kv_update_k4v2, hmma_loader.py:40-43;
+ * the reference names it but no caller shows its symbol, so it takes the
+ * fused encode's arguments). */
+int cda_paged_encode_fused_k4v2(const void *k, const void *v, int64_t k_stride,
+                                int64_t v_stride, const int32_t *slot_mapping,
+                                int64_t num_tokens, void *flat_cache, int64_t num_slots,
+                                int slot_bytes, int H_kv, const float *cb_k, const float *cb_v,
+                                void *stream);
 
 /* --------------------------------------------------------------- prefill --
  * Causal varlen prefill with the Hadamard-128 rotation of Q fused in front and
@@ -231,6 +256,18 @@ int cda_fa2_paged_cache_to_dense_rotated(const void *kv_cache, int64_t num_slots
                                          const float *cb_v, int levels, int block_size,
                                          int max_seq_len, void *k_out, void *v_out,
                                          void *stream);
+
+/* cda_fa2_paged_cache_to_dense_rotated for the legacy K4V2 cache (the module
+ * of load_fa2_cda_loader(k4v2=True), _v1_fa2_cda_loader_k4v2,
+ * hmma_loader.py:46-49, called by fa2_cda.py:64-95): V rows decoded from the
+ * 2-bit codes with the 4-level cb_v. */
+int cda_fa2_paged_cache_to_dense_rotated_k4v2(const void *kv_cache, int64_t num_slots,
+                                              int slot_bytes, int H_kv,
+                                              const int32_t *block_table, int bt_stride,
+                                              const int32_t *seq_lens, int B, const float *cb_k,
+                                              const float *cb_v, int block_size,
+                                              int max_seq_len, void *k_out, void *v_out,
+                                              void *stream);
 
 /* Replaces the reference pybind function hadamard128_fp16(x, y, scale)
  * (cda/kernels_cuda/fa2_cda.py:51-52, module _v1_fa2_cda_hadamard128):

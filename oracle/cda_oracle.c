@@ -268,15 +268,29 @@ void cda_oracle_decode_rows(const uint8_t *packed, const float *norm, int64_t ro
 
 /* ------------------------------------------------- paged decode attention -- */
 
-/* Slot layout (cda_attn_v2.py:20-27, generalised to 2-bit):
-   [K codes kb | V codes kb | K norm f32 | V norm f32 | pad], kb = 128*bits/8. */
+/* Slot layout (cda_attn_v2.py:20-29, generalised to 2-bit codes):
+   [K codes kbk | V codes kbv | K norm f32 | V norm f32 | pad], kb = 128*bits/8:
+   K4V4 64 | 64 (144-byte slots), K2V2 32 | 32, K4V2 64 | 32 (the legacy
+   104-byte slot).  The level argument L of the paged functions below is the
+   K codebook size, with the V codebook size in bits 8..15 when it differs. */
 typedef struct {
     const uint8_t *kv;
     int64_t row_bytes;   /* H_kv * slot_bytes */
     int slot_bytes;
-    int kb;
-    int bits;
+    int kbk, kbv;
+    int bitsk, bitsv;
 } cache_view;
+
+static void init_view(cache_view *c, const uint8_t *kv, int H_kv, int slot_bytes, int L) {
+    const int lk = L & 0xFF, lv = (L >> 8) ? (L >> 8) : lk;
+    c->kv = kv;
+    c->slot_bytes = slot_bytes;
+    c->row_bytes = (int64_t)H_kv * slot_bytes;
+    c->bitsk = lk == 16 ? 4 : 2;
+    c->bitsv = lv == 16 ? 4 : 2;
+    c->kbk = D * c->bitsk / 8;
+    c->kbv = D * c->bitsv / 8;
+}
 
 static const uint8_t *slot_ptr(const cache_view *c, int64_t slot, int h) {
     return c->kv + slot * c->row_bytes + (int64_t)h * c->slot_bytes;
@@ -300,8 +314,9 @@ static void decode_window(const cache_view *c, const int32_t *bt_row, int block_
     for (int t = k0; t < k1; ++t) {
         int64_t slot = (int64_t)bt_row[t / block_size] * block_size + t % block_size;
         const uint8_t *p = slot_ptr(c, slot, h);
-        decode_row(p, load_f32(p + 2 * c->kb), cbK, c->bits, K + (int64_t)(t - k0) * D);
-        decode_row(p + c->kb, load_f32(p + 2 * c->kb + 4), cbV, c->bits, V + (int64_t)(t - k0) * D);
+        const uint8_t *nrm = p + c->kbk + c->kbv;
+        decode_row(p, load_f32(nrm), cbK, c->bitsk, K + (int64_t)(t - k0) * D);
+        decode_row(p + c->kbk, load_f32(nrm + 4), cbV, c->bitsv, V + (int64_t)(t - k0) * D);
     }
 }
 
@@ -360,11 +375,7 @@ void cda_oracle_decode_paged(const uint16_t *q, const uint8_t *kv, int H_kv, int
                              const float *cbK, const float *cbV, const float *R, float scale,
                              int rotated_io, uint16_t *out) {
     cache_view c;
-    c.kv = kv;
-    c.slot_bytes = slot_bytes;
-    c.row_bytes = (int64_t)H_kv * slot_bytes;
-    c.bits = (L == 16) ? 4 : 2;
-    c.kb = D * c.bits / 8;
+    init_view(&c, kv, H_kv, slot_bytes, L);
     const int g = H_q / H_kv;
 #pragma omp parallel for collapse(2) schedule(dynamic)
     for (int b = 0; b < B; ++b)
@@ -401,11 +412,7 @@ void cda_oracle_decode_partial(const uint16_t *q_rot, const uint8_t *kv, int H_k
                                const float *cbK, const float *cbV, float scale, int k0, int k1,
                                float *o_un, float *m_out, float *l_out) {
     cache_view c;
-    c.kv = kv;
-    c.slot_bytes = slot_bytes;
-    c.row_bytes = (int64_t)H_kv * slot_bytes;
-    c.bits = (L == 16) ? 4 : 2;
-    c.kb = D * c.bits / 8;
+    init_view(&c, kv, H_kv, slot_bytes, L);
     const int g = H_q / H_kv;
     for (int b = 0; b < B; ++b)
         for (int h = 0; h < H_kv; ++h) {
@@ -442,11 +449,7 @@ void cda_oracle_prefill_paged(const uint16_t *q, const int32_t *cu_q, const uint
                               const float *cbK, const float *cbV, const float *R, float scale,
                               uint16_t *out) {
     cache_view c;
-    c.kv = kv;
-    c.slot_bytes = slot_bytes;
-    c.row_bytes = (int64_t)H_kv * slot_bytes;
-    c.bits = (L == 16) ? 4 : 2;
-    c.kb = D * c.bits / 8;
+    init_view(&c, kv, H_kv, slot_bytes, L);
     const int g = H_q / H_kv;
     for (int b = 0; b < B; ++b) {
         int M = cu_q[b + 1] - cu_q[b];

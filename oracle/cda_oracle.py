@@ -148,21 +148,31 @@ def decode_rotated(packed: np.ndarray, norm: np.ndarray, cb: np.ndarray) -> np.n
 
 # ------------------------------------------------------------- paged cache --
 
-def slot_layout(L: int, slot_bytes: int | None = None):
+def slot_layout(L: int, slot_bytes: int | None = None, Lv: int | None = None):
     """(code bytes per role, slot bytes).  K4V4: 64, 144 (cda_attn_v2.py:52-60);
-    K2V2: 32, 80."""
+    K2V2: 32, 80; K4V2 (Lv = 4): 64, 104 (the legacy layout, cda_attn_v2.py:29,
+    K codes | V codes | K norm | V norm with no padding)."""
     kb = D * (4 if L == 16 else 2) // 8
+    if Lv is not None and Lv != L:
+        kbv = D * (4 if Lv == 16 else 2) // 8
+        return kb, (slot_bytes if slot_bytes else kb + kbv + 8)
     data = 2 * kb + 8
     return kb, (slot_bytes if slot_bytes else (data + 15) // 16 * 16)
 
 
+def _levels_arg(cbK, cbV):
+    """Level argument of the C paged functions: K size, V size in bits 8..15."""
+    return cbK.size if cbV.size == cbK.size else cbK.size | (cbV.size << 8)
+
+
 def build_paged_cache(k_idx, k_norm, v_idx, v_norm, block_table, block_size, L,
-                      num_blocks=None, slot_bytes=None, fill=0):
+                      num_blocks=None, slot_bytes=None, fill=0, Lv=None):
     """Scatter (B, H_kv, N, kb)/(B, H_kv, N) encodings into a
     (num_blocks*block_size, H_kv, slot_bytes) uint8 cache through block_table."""
     B, H_kv, N, kb = k_idx.shape
-    kb2, sb = slot_layout(L, slot_bytes)
+    kb2, sb = slot_layout(L, slot_bytes, Lv)
     assert kb == kb2
+    kbv = v_idx.shape[-1]
     if num_blocks is None:
         num_blocks = int(block_table.max()) + 1
     cache = np.full((num_blocks * block_size, H_kv, sb), fill, dtype=np.uint8)
@@ -170,10 +180,10 @@ def build_paged_cache(k_idx, k_norm, v_idx, v_norm, block_table, block_size, L,
     for b in range(B):
         slots = block_table[b, t // block_size].astype(np.int64) * block_size + t % block_size
         cache[slots, :, 0:kb] = k_idx[b].transpose(1, 0, 2)
-        cache[slots, :, kb:2 * kb] = v_idx[b].transpose(1, 0, 2)
-        cache[slots, :, 2 * kb:2 * kb + 4] = (
+        cache[slots, :, kb:kb + kbv] = v_idx[b].transpose(1, 0, 2)
+        cache[slots, :, kb + kbv:kb + kbv + 4] = (
             np.ascontiguousarray(k_norm[b].T.astype(np.float32)).view(np.uint8).reshape(N, H_kv, 4))
-        cache[slots, :, 2 * kb + 4:2 * kb + 8] = (
+        cache[slots, :, kb + kbv + 4:kb + kbv + 8] = (
             np.ascontiguousarray(v_norm[b].T.astype(np.float32)).view(np.uint8).reshape(N, H_kv, 4))
     return cache
 
@@ -195,7 +205,7 @@ def decode_paged(q, cache, block_table, seq_lens, cbK, cbV, R, *, H_kv, block_si
         scale = 1.0 / np.sqrt(D)
     out = np.empty((B, H_q, D), dtype=np.uint16)
     lib().cda_oracle_decode_paged(_p(q.view(np.uint16)), _p(cache), H_kv, cache.shape[-1],
-                                  cbK.size, _p(bt), bt.shape[1], _p(sl), B, H_q, block_size,
+                                  _levels_arg(cbK, cbV), _p(bt), bt.shape[1], _p(sl), B, H_q, block_size,
                                   _p(cbK), _p(cbV), _p(R), float(scale), int(rotated_io),
                                   _p(out))
     return out.view(np.float16)
@@ -217,7 +227,7 @@ def decode_partial(q_rot, cache, block_table, seq_lens, cbK, cbV, *, H_kv, block
     m = np.empty((B, H_q), dtype=np.float32)
     l = np.empty((B, H_q), dtype=np.float32)
     lib().cda_oracle_decode_partial(_p(q_rot.view(np.uint16)), _p(cache), H_kv, cache.shape[-1],
-                                    cbK.size, _p(bt), bt.shape[1], _p(sl), B, H_q, block_size,
+                                    _levels_arg(cbK, cbV), _p(bt), bt.shape[1], _p(sl), B, H_q, block_size,
                                     _p(cbK), _p(cbV), float(scale), int(k0), int(k1),
                                     _p(o), _p(m), _p(l))
     return o, m, l
@@ -239,7 +249,7 @@ def prefill_paged(q, cu_q, cache, block_table, seq_lens, cbK, cbV, R, *, H_kv, b
         scale = 1.0 / np.sqrt(D)
     out = np.empty((T, H_q, D), dtype=np.uint16)
     lib().cda_oracle_prefill_paged(_p(q.view(np.uint16)), _p(cu), _p(cache), H_kv,
-                                   cache.shape[-1], cbK.size, _p(bt), bt.shape[1], _p(sl),
+                                   cache.shape[-1], _levels_arg(cbK, cbV), _p(bt), bt.shape[1], _p(sl),
                                    len(cu) - 1, H_q, block_size, _p(cbK), _p(cbV), _p(R),
                                    float(scale), _p(out))
     return out.view(np.float16)

@@ -28,6 +28,9 @@ SYMBOLS = (
     "cda_decode_full_hmma_v3",
     "cda_decode_set_timing_events",
     "cda_decode_set_stream_kernel",
+    "cda_decode_full_hmma_v3_k4v2",
+    "cda_paged_encode_fused_k4v2",
+    "cda_fa2_paged_cache_to_dense_rotated_k4v2",
     "cda_decode_noalloc_max_workspace",
     "cda_decode_full_hmma_v3_noalloc",
     "cda_paged_encode_fused",
@@ -96,6 +99,16 @@ def lib():
         L.cda_decode_set_timing_events.argtypes = [_P, _P]
         L.cda_decode_set_stream_kernel.restype = _I32
         L.cda_decode_set_stream_kernel.argtypes = [_I32]
+        L.cda_decode_full_hmma_v3_k4v2.restype = _I32
+        L.cda_decode_full_hmma_v3_k4v2.argtypes = [
+            _P, _P, _I64, _I32, _I32, _P, _I32, _P, _P, _P, _P, _P, _P,
+            _I32, _I32, _I32, _I32, _I32, _I32, _F32, _P, _SZ, _P]
+        L.cda_paged_encode_fused_k4v2.restype = _I32
+        L.cda_paged_encode_fused_k4v2.argtypes = [
+            _P, _P, _I64, _I64, _P, _I64, _P, _I64, _I32, _I32, _P, _P, _P]
+        L.cda_fa2_paged_cache_to_dense_rotated_k4v2.restype = _I32
+        L.cda_fa2_paged_cache_to_dense_rotated_k4v2.argtypes = [
+            _P, _I64, _I32, _I32, _P, _I32, _P, _I32, _P, _P, _I32, _I32, _P, _P, _P]
         L.cda_paged_encode_fused.restype = _I32
         L.cda_paged_encode_fused.argtypes = [
             _P, _P, _I64, _I64, _P, _I64, _P, _I64, _I32, _I32, _P, _P, _I32, _P]
@@ -198,8 +211,10 @@ def decode(q: torch.Tensor, kv_cache: torch.Tensor, block_table: torch.Tensor,
         raise ValueError("block_table must be (B, max_blocks) with unit inner stride")
     if rot_f32.shape != (128, 128) or not rot_f32.is_contiguous():
         raise ValueError("rot_f32 must be a contiguous (128, 128) tensor")
-    if cb_k.numel() != cb_v.numel():
-        raise ValueError("cb_K and cb_V must have the same number of levels")
+    k4v2 = (cb_k.numel(), cb_v.numel()) == (16, 4)
+    if cb_k.numel() != cb_v.numel() and not k4v2:
+        raise ValueError("cb_K and cb_V must have the same number of levels (or 16 and 4: the "
+                         "K4V2 cache)")
     B, H_q, _ = q.shape
     num_slots, H_kv, slot_bytes = kv_cache.shape
     if block_table.shape[0] < B or seq_lens.numel() < B:
@@ -212,6 +227,15 @@ def decode(q: torch.Tensor, kv_cache: torch.Tensor, block_table: torch.Tensor,
         workspace = torch.empty(need + 256, dtype=torch.uint8, device=dev)
     ws_ptr = workspace.data_ptr()
     pad = (-ws_ptr) % 256
+    if k4v2:
+        rc = lib().cda_decode_full_hmma_v3_k4v2(
+            _ptr(q), _ptr(kv_cache), num_slots, slot_bytes, H_kv, _ptr(block_table),
+            block_table.stride(0), _ptr(seq_lens), _ptr(cb_k), _ptr(cb_v), _ptr(rot_f32),
+            _ptr(rot_f16), _ptr(out), B, H_q, int(group_size), int(block_size), int(tile_n),
+            int(max_seq_len), float(scale), ctypes.c_void_p(ws_ptr + pad),
+            workspace.numel() - pad, _stream(dev))
+        _check(rc, "cda_decode_full_hmma_v3_k4v2")
+        return
     rc = lib().cda_decode_full_hmma_v3(
         _ptr(q), _ptr(kv_cache), num_slots, slot_bytes, H_kv, _ptr(block_table),
         block_table.stride(0), _ptr(seq_lens), _ptr(cb_k), _ptr(cb_v),
@@ -269,8 +293,16 @@ def paged_encode(k: torch.Tensor, v: torch.Tensor, slot_mapping: torch.Tensor,
     if slot_mapping.numel() < T:
         raise ValueError("slot_mapping shorter than the number of tokens")
     levels = cb_k.numel()
+    if (levels, cb_v.numel()) == (16, 4):        # the legacy K4V2 slot
+        rc = lib().cda_paged_encode_fused_k4v2(
+            _ptr(k), _ptr(v), k.stride(0), v.stride(0), _ptr(slot_mapping.contiguous()), T,
+            _ptr(flat_cache), flat_cache.shape[0], flat_cache.shape[2], H_kv,
+            _ptr(cb_k.float().contiguous()), _ptr(cb_v.float().contiguous()), _stream(dev))
+        _check(rc, "cda_paged_encode_fused_k4v2")
+        return
     if cb_v.numel() != levels or levels not in (4, 16):
-        raise ValueError("cb_K and cb_V must both have 16 (K4V4) or 4 (K2V2) levels")
+        raise ValueError("cb_K and cb_V must both have 16 (K4V4) or 4 (K2V2) levels, or 16 and "
+                         "4 (K4V2)")
     rc = lib().cda_paged_encode_fused(
         _ptr(k), _ptr(v), k.stride(0), v.stride(0), _ptr(slot_mapping.contiguous()), T,
         _ptr(flat_cache), flat_cache.shape[0], flat_cache.shape[2], H_kv,
@@ -280,13 +312,15 @@ def paged_encode(k: torch.Tensor, v: torch.Tensor, slot_mapping: torch.Tensor,
 
 # ----------------------------------------------------------------- prefill --
 
-def _check_paged(kv_cache, block_table, seq_lens, cb_k, cb_v):
+def _check_paged(kv_cache, block_table, seq_lens, cb_k, cb_v, allow_k4v2=False):
     if kv_cache.dtype != torch.uint8 or kv_cache.dim() != 3 or not kv_cache.is_contiguous():
         raise ValueError("kv_cache must be a contiguous uint8 (num_slots, H_kv, slot_bytes) tensor")
     if block_table.dtype != torch.int32 or block_table.dim() != 2 or block_table.stride(1) != 1:
         raise ValueError("block_table must be int32 (B, max_blocks) with unit inner stride")
     if seq_lens.dtype != torch.int32:
         raise TypeError("seq_lens must be int32")
+    if allow_k4v2 and (cb_k.numel(), cb_v.numel()) == (16, 4):
+        return
     if cb_k.numel() != 16 or cb_v.numel() != 16:
         raise ValueError("the prefill kernels read K4V4 caches (16-level codebooks)")
 
@@ -452,11 +486,19 @@ def paged_to_dense(kv_cache: torch.Tensor, block_table: torch.Tensor, seq_lens: 
     """Dense rotated fp16 K/V, (B * max_seq_len, H_kv, 128) each, zero past
     seq_lens (fa2_cda.py:64-95)."""
     dev = _require_gpu(kv_cache, block_table, seq_lens, cb_k, cb_v)
-    _check_paged(kv_cache, block_table, seq_lens, cb_k, cb_v)
+    _check_paged(kv_cache, block_table, seq_lens, cb_k, cb_v, allow_k4v2=True)
     B = seq_lens.numel()
     num_slots, H_kv, slot_bytes = kv_cache.shape
     k_out = torch.empty(B * max_seq_len, H_kv, 128, dtype=torch.float16, device=dev)
     v_out = torch.empty_like(k_out)
+    if (cb_k.numel(), cb_v.numel()) == (16, 4):  # the legacy K4V2 slot
+        rc = lib().cda_fa2_paged_cache_to_dense_rotated_k4v2(
+            _ptr(kv_cache), num_slots, slot_bytes, H_kv, _ptr(block_table),
+            block_table.stride(0), _ptr(seq_lens), B, _ptr(cb_k.float().contiguous()),
+            _ptr(cb_v.float().contiguous()), int(block_size), int(max_seq_len), _ptr(k_out),
+            _ptr(v_out), _stream(dev))
+        _check(rc, "cda_fa2_paged_cache_to_dense_rotated_k4v2")
+        return k_out, v_out
     rc = lib().cda_fa2_paged_cache_to_dense_rotated(
         _ptr(kv_cache), num_slots, slot_bytes, H_kv, _ptr(block_table), block_table.stride(0),
         _ptr(seq_lens), B, _ptr(cb_k.float().contiguous()), _ptr(cb_v.float().contiguous()), 16,

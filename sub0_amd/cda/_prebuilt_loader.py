@@ -24,8 +24,10 @@ import torch
 from sub0_amd import _native
 
 _DECODE_NAMES = {
-    "_v1_decode_hmma_k4v4_gs4": 4,
-    "_v1_decode_hmma_k4v4_gs8": 8,
+    "_v1_decode_hmma_k4v4_gs4": (4, False),
+    "_v1_decode_hmma_k4v4_gs8": (8, False),
+    "_v1_decode_hmma_k4v2_gs4": (4, True),
+    "_v1_decode_hmma_k4v2_gs8": (8, True),
 }
 
 
@@ -48,10 +50,10 @@ def _flat_cache(kv_cache: torch.Tensor) -> torch.Tensor:
     return kv_cache
 
 
-def _make_decode_module(name: str, gs: int) -> ModuleType:
+def _make_decode_module(name: str, gs: int, k4v2: bool) -> ModuleType:
     mod = ModuleType(name)
-    mod.__doc__ = ("CDA split-K decode (K4V4, group size %d) on MI355X; replaces the "
-                   "reference's %s.so." % (gs, name))
+    mod.__doc__ = ("CDA split-K decode (%s, group size %d) on MI355X; replaces the "
+                   "reference's %s.so." % ("K4V2, 104-byte slots" if k4v2 else "K4V4", gs, name))
 
     def cda_decode_full_hmma_v3(Q, kv_cache, block_table, seq_lens, cb_K, cb_V,
                                 rotation_fp32, rotation_fp16, out, group_size, block_size,
@@ -59,6 +61,8 @@ def _make_decode_module(name: str, gs: int) -> ModuleType:
         """Positional signature of the reference call (wrappers.py:115-124)."""
         if int(group_size) != gs:
             raise ValueError(f"{name} is built for group_size={gs}, got {group_size}")
+        if k4v2 and (cb_K.numel(), cb_V.numel()) != (16, 4):
+            raise ValueError(f"{name} reads K4V2 caches: cb_K needs 16 levels, cb_V 4")
         torch.ops.cda_hip.decode(
             Q, _flat_cache(kv_cache), block_table, seq_lens, cb_K, cb_V, rotation_fp32,
             rotation_fp16 if rotation_fp16 is not None else rotation_fp32, out, gs,
@@ -71,7 +75,8 @@ def _make_decode_module(name: str, gs: int) -> ModuleType:
 
 def _make_encode_module(name: str) -> ModuleType:
     mod = ModuleType(name)
-    mod.__doc__ = "CDA fused paged encode (K4V4 and K2V2) on MI355X."
+    mod.__doc__ = ("CDA fused paged encode on MI355X: K4V4 and K2V2 slots, or the legacy "
+                   "K4V2 slot when cb_V has 4 levels and cb_K 16.")
 
     def cda_paged_encode_fused(K, V, slot_mapping, flat_cache, cb_K, cb_V):
         """Positional signature of the reference call (wrappers.py:153-156)."""
@@ -86,8 +91,11 @@ def _register_ops():
 
 
 def _factories():
-    f = {n: (lambda n=n, g=g: _make_decode_module(n, g)) for n, g in _DECODE_NAMES.items()}
-    f["_v1_paged_encode_fused"] = lambda: _make_encode_module("_v1_paged_encode_fused")
+    f = {n: (lambda n=n, g=g: _make_decode_module(n, *g)) for n, g in _DECODE_NAMES.items()}
+    # The kv-update modules (hmma_loader.py:40-43) have no caller in the
+    # reference that shows their symbol; they carry the fused encode.
+    for n in ("_v1_paged_encode_fused", "_v1_kv_update_k4v4", "_v1_kv_update_k4v2"):
+        f[n] = lambda n=n: _make_encode_module(n)
     try:
         from sub0_amd.cda.kernels_cuda import _prefill_modules
     except ImportError:

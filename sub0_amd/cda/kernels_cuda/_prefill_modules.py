@@ -19,7 +19,8 @@ def _flat_cache(kv_cache):
 
 def _loader_module(name: str) -> ModuleType:
     mod = ModuleType(name)
-    mod.__doc__ = "Paged K4V4 cache -> dense rotated fp16 K/V (MI355X)."
+    mod.__doc__ = ("Paged K4V4 (or, with a 4-level cb_V, the legacy K4V2) cache -> dense "
+                   "rotated fp16 K/V (MI355X).")
 
     def cda_fa2_paged_cache_to_dense_rotated(kv_cache, block_table, seq_lens, cb_K, cb_V,
                                              block_size, max_seq_len):
@@ -59,6 +60,7 @@ def _hadamard_module(name: str) -> ModuleType:
 
 FACTORIES = {
     "_v1_fa2_cda_loader_k4v4": lambda: _loader_module("_v1_fa2_cda_loader_k4v4"),
+    "_v1_fa2_cda_loader_k4v2": lambda: _loader_module("_v1_fa2_cda_loader_k4v2"),
     "_v1_fa2_cda_varlen_fused": lambda: _varlen_module("_v1_fa2_cda_varlen_fused"),
     "_v1_fa2_cda_hadamard128": lambda: _hadamard_module("_v1_fa2_cda_hadamard128"),
 }

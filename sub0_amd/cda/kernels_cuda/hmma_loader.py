@@ -2,8 +2,8 @@
 
 Same names and argument checks as the reference (``hmma_loader.py:27-59``);
 each resolves through :func:`sub0_amd.cda._prebuilt_loader.load_pybind_module`
-to the MI355X HIP library.  Names the MI355X build does not provide (the
-K4V2 decode and the legacy kv-update kernels) raise ``PrebuiltMissing``.
+to the MI355X HIP library, including the K4V2 names (decode, kv update and
+dense loader of the legacy 104-byte slot).
 """
 from __future__ import annotations
 

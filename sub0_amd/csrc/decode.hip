@@ -151,11 +151,11 @@ __device__ __forceinline__ uint32_t widen_2bit(uint32_t x) {
            ((y << 8) & 0x03000300u);
 }
 
-// One 16-token tile of a chunk.  L = 16: 16 K bytes and 4 V bytes per lane;
-// L = 4: 8 and 2, widened to the 4-bit layout.
-template <int L>
+// One 16-token tile of a chunk.  K: 16 code bytes per lane (LK = 16) or 8
+// widened to the 4-bit layout (LK = 4); V likewise 4 or 2 bytes per token.
+template <int LK, int LV>
 __device__ __forceinline__ void load_tile(Chunk &c, int t, rsrc_t r, const LaneOffsets &o) {
-    if constexpr (L == 16) {
+    if constexpr (LK == 16) {
         c.kq[t] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, o.k, 0, 0));
     } else {
         typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
@@ -166,7 +166,7 @@ __device__ __forceinline__ void load_tile(Chunk &c, int t, rsrc_t r, const LaneO
     c.nk[t] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, o.nk, 0, 0));
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        if constexpr (L == 16)
+        if constexpr (LV == 16)
             c.vw[t][i] = __builtin_amdgcn_raw_buffer_load_b32(r, o.v[i], 0, 0);
         else
             c.vw[t][i] = widen_2bit(__builtin_amdgcn_raw_buffer_load_b16(r, o.v[i], 0, 0));
@@ -174,7 +174,7 @@ __device__ __forceinline__ void load_tile(Chunk &c, int t, rsrc_t r, const LaneO
     }
 }
 
-template <int GS, int L>
+template <int GS, int LK, int LV>
 __global__ void __launch_bounds__(kThreads, 1)
 decode_split_kernel(SplitParams p) {
     if (p.cb_same && *p.cb_same) return;        // the page-streaming kernel covers this call
@@ -193,7 +193,7 @@ decode_split_kernel(SplitParams p) {
         // stay below 4); they are set to 0 rather than read out of bounds.
         if (tid < 32) {
             const int e = tid & 15;
-            cbs[tid >> 4][e] = (e < L) ? ((tid < 16) ? p.cb_k[e] : p.cb_v[e]) : 0.0f;
+            cbs[tid >> 4][e] = (tid < 16) ? (e < LK ? p.cb_k[e] : 0.0f) : (e < LV ? p.cb_v[e] : 0.0f);
         }
         __syncthreads();
         for (int i = tid; i < kLutDwords / 2; i += kThreads) {
@@ -241,14 +241,16 @@ decode_split_kernel(SplitParams p) {
 
     const uint32_t colK = (uint32_t)(lane & 31) * 8u;
     const uint32_t colV = 0x10000u | ((uint32_t)(lane & 31) * 8u);
-    constexpr int KB = (L == 16) ? kD / 2 : kD / 4;     // code bytes per role
+    // Slot: [K codes KBK | V codes KBV | K norm | V norm | pad].
+    constexpr int KBK = (LK == 16) ? kD / 2 : kD / 4;
+    constexpr int KBV = (LV == 16) ? kD / 2 : kD / 4;
     LaneOffsets lo;
-    lo.k = (uint32_t)(r16 * p.row_bytes + q4 * (KB / 4));
-    lo.nk = (uint32_t)(r16 * p.row_bytes + 2 * KB);
+    lo.k = (uint32_t)(r16 * p.row_bytes + q4 * (KBK / 4));
+    lo.nk = (uint32_t)(r16 * p.row_bytes + KBK + KBV);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        lo.v[i] = (uint32_t)((4 * q4 + i) * p.row_bytes + KB + (KB / 16) * r16);
-        lo.nv[i] = (uint32_t)((4 * q4 + i) * p.row_bytes + 2 * KB + 4);
+        lo.v[i] = (uint32_t)((4 * q4 + i) * p.row_bytes + KBK + (KBV / 16) * r16);
+        lo.nv[i] = (uint32_t)((4 * q4 + i) * p.row_bytes + KBK + KBV + 4);
     }
     const int32_t *bt = p.block_table + (int64_t)b * p.bt_stride;
     const uint8_t *kvh = p.kv + (int64_t)h * p.slot_bytes;
@@ -265,8 +267,8 @@ decode_split_kernel(SplitParams p) {
     auto load_chunk = [&](Chunk &c, int c0) {
         const rsrc_t r0 = tile_res(c0);
         const rsrc_t r1 = (c0 + 16 < end) ? tile_res(c0 + 16) : r0;
-        load_tile<L>(c, 0, r0, lo);
-        load_tile<L>(c, 1, r1, lo);
+        load_tile<LK, LV>(c, 0, r0, lo);
+        load_tile<LK, LV>(c, 1, r1, lo);
     };
 
     floatx4 acc_o[8];
@@ -1218,46 +1220,44 @@ extern "C" size_t cda_decode_workspace_size(int B, int H_q, int H_kv, int max_se
     return ws_layout(B, H_q, ns).total;
 }
 
-extern "C" int cda_decode_full_hmma_v3(const void *q, const void *kv_cache, int64_t num_slots,
-                                       int slot_bytes, int H_kv, const int32_t *block_table,
-                                       int bt_stride, const int32_t *seq_lens, const float *cb_k,
-                                       const float *cb_v, int levels, const float *rot_f32,
-                                       const void *rot_f16, void *out, int B, int H_q,
-                                       int group_size, int block_size, int tile_n,
-                                       int max_seq_len, float scale, void *workspace,
-                                       size_t workspace_bytes, void *stream) {
-    (void)rot_f16;
-    (void)num_slots;
+namespace cda {
+namespace {
+// Shared body of the decode entry points.  levels_k / levels_v: 16/16 (K4V4),
+// 4/4 (K2V2) or 16/4 (the legacy K4V2 104-byte slot).
+int decode_impl(const void *q, const void *kv_cache, int slot_bytes, int H_kv,
+                const int32_t *block_table, int bt_stride, const int32_t *seq_lens,
+                const float *cb_k, const float *cb_v, int levels_k, int levels_v,
+                const float *rot_f32, void *out, int B, int H_q, int group_size, int block_size,
+                int tile_n, int max_seq_len, float scale, void *workspace,
+                size_t workspace_bytes, void *stream, const char *fn) {
+    const std::string f(fn);
     CDA_REQUIRE(q && kv_cache && block_table && seq_lens && cb_k && cb_v && rot_f32 && out,
-                "cda_decode_full_hmma_v3: null pointer argument");
-    CDA_REQUIRE(B > 0 && H_kv > 0 && H_q > 0, "cda_decode_full_hmma_v3: B, H_q, H_kv must be > 0");
-    CDA_REQUIRE(group_size == 4 || group_size == 8,
-                "cda_decode_full_hmma_v3: group_size must be 4 or 8");
-    CDA_REQUIRE(H_q == H_kv * group_size,
-                "cda_decode_full_hmma_v3: H_q must equal H_kv * group_size");
-    CDA_REQUIRE(levels == 16 || levels == 4,
-                "cda_decode_full_hmma_v3: codebooks must have 16 levels (K4V4) or 4 (K2V2)");
-    const int code_bytes = (levels == 16) ? kD / 2 : kD / 4;
-    CDA_REQUIRE(slot_bytes >= 2 * code_bytes + 8 && slot_bytes % 16 == 0,
-                "cda_decode_full_hmma_v3: slot_bytes must hold both code fields and the two "
-                "norms (>= 136 for K4V4, >= 72 for K2V2) and be a multiple of 16");
+                f + ": null pointer argument");
+    CDA_REQUIRE(B > 0 && H_kv > 0 && H_q > 0, f + ": B, H_q, H_kv must be > 0");
+    CDA_REQUIRE(group_size == 4 || group_size == 8, f + ": group_size must be 4 or 8");
+    CDA_REQUIRE(H_q == H_kv * group_size, f + ": H_q must equal H_kv * group_size");
+    const int kbk = (levels_k == 16) ? kD / 2 : kD / 4;
+    const int kbv = (levels_v == 16) ? kD / 2 : kD / 4;
+    const int align = (levels_k == levels_v) ? 16 : 8;
+    CDA_REQUIRE(slot_bytes >= kbk + kbv + 8 && slot_bytes % align == 0,
+                f + ": slot_bytes must hold both code fields and the two norms (>= 136 for "
+                    "K4V4, >= 72 for K2V2, a multiple of 16; >= 104 and a multiple of 8 for "
+                    "K4V2)");
     CDA_REQUIRE(block_size > 0 && block_size % 16 == 0,
-                "cda_decode_full_hmma_v3: block_size must be a positive multiple of 16");
-    CDA_REQUIRE(max_seq_len >= 0 && bt_stride > 0,
-                "cda_decode_full_hmma_v3: bad max_seq_len / block-table stride");
-    CDA_REQUIRE((int64_t)16 * H_kv * slot_bytes < (int64_t)1 << 31,
-                "cda_decode_full_hmma_v3: cache row too wide");
+                f + ": block_size must be a positive multiple of 16");
+    CDA_REQUIRE(max_seq_len >= 0 && bt_stride > 0, f + ": bad max_seq_len / block-table stride");
+    CDA_REQUIRE((int64_t)16 * H_kv * slot_bytes < (int64_t)1 << 31, f + ": cache row too wide");
     CDA_REQUIRE(((uintptr_t)kv_cache & 15) == 0 && ((uintptr_t)q & 15) == 0,
-                "cda_decode_full_hmma_v3: q and kv_cache must be 16-byte aligned");
+                f + ": q and kv_cache must be 16-byte aligned");
     int tn = 0, ns = 0;
     int rc = cda_decode_plan(B, H_q, H_kv, max_seq_len, tile_n, &tn, &ns);
     if (rc) return rc;
-    CDA_REQUIRE(ns <= kMaxSplits, "cda_decode_full_hmma_v3: tile_n gives more than 1024 "
-                                  "context splits; use a larger tile_n");
+    CDA_REQUIRE(ns <= kMaxSplits, f + ": tile_n gives more than 1024 context splits; use a "
+                                      "larger tile_n");
     const WsLayout w = ws_layout(B, H_q, ns);
     if (!workspace || workspace_bytes < w.total || ((uintptr_t)workspace & 255))
-        return fail(CDA_E_WORKSPACE, "cda_decode_full_hmma_v3: workspace missing, misaligned or "
-                                     "smaller than cda_decode_workspace_size()");
+        return fail(CDA_E_WORKSPACE, f + ": workspace missing, misaligned or smaller than "
+                                         "cda_decode_workspace_size()");
     char *ws = static_cast<char *>(workspace);
     hipStream_t st = static_cast<hipStream_t>(stream);
 
@@ -1269,14 +1269,14 @@ extern "C" int cda_decode_full_hmma_v3(const void *q, const void *kv_cache, int6
     // rotation kernel compares them on the device and both split kernels are
     // launched, each returning at once unless the comparison picks it (no
     // host round trip, so the choice is the same inside graph capture).
-    const bool stream_shape = H_kv == 8 &&
-                              ((levels == 16 && slot_bytes == 144) ||
-                               (levels == 4 && slot_bytes == 80)) &&
+    const bool stream_shape = H_kv == 8 && levels_k == levels_v &&
+                              ((levels_k == 16 && slot_bytes == 144) ||
+                               (levels_k == 4 && slot_bytes == 80)) &&
                               tn <= 16 * kStreamMaxPages && g_allow_stream;
     const bool dual = stream_shape && cb_k != cb_v;
     int *cb_same = dual ? reinterpret_cast<int *>(ws + w.flag) : nullptr;
     rotate_q_kernel<<<head_grid, 256, 0, st>>>(static_cast<const uint16_t *>(q), rot_f32, q_rot,
-                                               H_q, cb_k, cb_v, levels, cb_same);
+                                               H_q, cb_k, cb_v, levels_k, cb_same);
     CDA_LAUNCH_CHECK("rotate_q_kernel");
 
     SplitParams p;
@@ -1297,14 +1297,14 @@ extern "C" int cda_decode_full_hmma_v3(const void *q, const void *kv_cache, int6
     p.tile_n = tn;
     p.n_splits = ns;
     p.scale_log2 = scale * kLog2e;
-    p.levels = levels;
+    p.levels = levels_k;
     p.cb_same = cb_same;
     dim3 grid(ns, (H_kv + kWaves - 1) / kWaves, B);
     const bool use_stream = stream_shape;
     if (g_split_start && hipEventRecord(g_split_start, st) != hipSuccess)
-        return fail(CDA_E_HIP, "cda_decode_full_hmma_v3: hipEventRecord(start) failed");
+        return fail(CDA_E_HIP, f + ": hipEventRecord(start) failed");
     if (use_stream) {
-        if (levels == 16) {
+        if (levels_k == 16) {
             if (group_size == 4)
                 decode_stream_kernel<4, 16><<<grid, kThreads, 0, st>>>(p);
             else
@@ -1317,20 +1317,25 @@ extern "C" int cda_decode_full_hmma_v3(const void *q, const void *kv_cache, int6
         }
     }
     if (!use_stream || dual) {
-        if (levels == 4) {
+        if (levels_k == 4) {
             if (group_size == 4)
-                decode_split_kernel<4, 4><<<grid, kThreads, 0, st>>>(p);
+                decode_split_kernel<4, 4, 4><<<grid, kThreads, 0, st>>>(p);
             else
-                decode_split_kernel<8, 4><<<grid, kThreads, 0, st>>>(p);
+                decode_split_kernel<8, 4, 4><<<grid, kThreads, 0, st>>>(p);
+        } else if (levels_v == 4) {
+            if (group_size == 4)
+                decode_split_kernel<4, 16, 4><<<grid, kThreads, 0, st>>>(p);
+            else
+                decode_split_kernel<8, 16, 4><<<grid, kThreads, 0, st>>>(p);
         } else if (group_size == 4) {
-            decode_split_kernel<4, 16><<<grid, kThreads, 0, st>>>(p);
+            decode_split_kernel<4, 16, 16><<<grid, kThreads, 0, st>>>(p);
         } else {
-            decode_split_kernel<8, 16><<<grid, kThreads, 0, st>>>(p);
+            decode_split_kernel<8, 16, 16><<<grid, kThreads, 0, st>>>(p);
         }
     }
     CDA_LAUNCH_CHECK("decode_split_kernel");
     if (g_split_stop && hipEventRecord(g_split_stop, st) != hipSuccess)
-        return fail(CDA_E_HIP, "cda_decode_full_hmma_v3: hipEventRecord(stop) failed");
+        return fail(CDA_E_HIP, f + ": hipEventRecord(stop) failed");
 
     // One head per block when four per block would leave CUs idle.
     if ((int64_t)head_grid.x * B < num_cus())
@@ -1341,6 +1346,43 @@ extern "C" int cda_decode_full_hmma_v3(const void *q, const void *kv_cache, int6
                                                      static_cast<uint16_t *>(out), H_q, ns);
     CDA_LAUNCH_CHECK("combine_kernel");
     return CDA_OK;
+}
+}  // namespace
+}  // namespace cda
+
+extern "C" int cda_decode_full_hmma_v3(const void *q, const void *kv_cache, int64_t num_slots,
+                                       int slot_bytes, int H_kv, const int32_t *block_table,
+                                       int bt_stride, const int32_t *seq_lens, const float *cb_k,
+                                       const float *cb_v, int levels, const float *rot_f32,
+                                       const void *rot_f16, void *out, int B, int H_q,
+                                       int group_size, int block_size, int tile_n,
+                                       int max_seq_len, float scale, void *workspace,
+                                       size_t workspace_bytes, void *stream) {
+    (void)rot_f16;
+    (void)num_slots;
+    CDA_REQUIRE(levels == 16 || levels == 4,
+                "cda_decode_full_hmma_v3: codebooks must have 16 levels (K4V4) or 4 (K2V2)");
+    return decode_impl(q, kv_cache, slot_bytes, H_kv, block_table, bt_stride, seq_lens, cb_k,
+                       cb_v, levels, levels, rot_f32, out, B, H_q, group_size, block_size, tile_n,
+                       max_seq_len, scale, workspace, workspace_bytes, stream,
+                       "cda_decode_full_hmma_v3");
+}
+
+extern "C" int cda_decode_full_hmma_v3_k4v2(const void *q, const void *kv_cache,
+                                            int64_t num_slots, int slot_bytes, int H_kv,
+                                            const int32_t *block_table, int bt_stride,
+                                            const int32_t *seq_lens, const float *cb_k,
+                                            const float *cb_v, const float *rot_f32,
+                                            const void *rot_f16, void *out, int B, int H_q,
+                                            int group_size, int block_size, int tile_n,
+                                            int max_seq_len, float scale, void *workspace,
+                                            size_t workspace_bytes, void *stream) {
+    (void)rot_f16;
+    (void)num_slots;
+    return decode_impl(q, kv_cache, slot_bytes, H_kv, block_table, bt_stride, seq_lens, cb_k,
+                       cb_v, 16, 4, rot_f32, out, B, H_q, group_size, block_size, tile_n,
+                       max_seq_len, scale, workspace, workspace_bytes, stream,
+                       "cda_decode_full_hmma_v3_k4v2");
 }
 
 extern "C" int cda_decode_set_timing_events(void *start_event, void *stop_event) {

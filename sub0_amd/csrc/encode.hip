@@ -166,22 +166,26 @@ struct EncLayout {
     static constexpr int kWaveFloats = V * kPitch + V * 16 + V * 8;
 };
 
-template <int L, int P>
+template <int LK, int LV, int P>
 __global__ void __launch_bounds__(64 * kEncWaves)
 paged_encode_kernel(EncodeParams p) {
     using Lay = EncLayout<P>;
     constexpr int V = Lay::V, M = Lay::M, PITCH = Lay::kPitch;
-    constexpr int KB = kD * (L == 16 ? 4 : 2) / 8;   // code bytes per role
+    // Slot: [K codes KBK | V codes KBV | K norm | V norm | pad].
+    constexpr int KBK = kD * (LK == 16 ? 4 : 2) / 8;
+    constexpr int KBV = kD * (LV == 16 ? 4 : 2) / 8;
     __shared__ double s_beta[2][16];
     __shared__ int s_strict[2][16];
     __shared__ float s_cb[2][16];
     __shared__ float s_w[kEncWaves][Lay::kWaveFloats];
 
-    if (threadIdx.x < 2 * L) {
-        const int r = threadIdx.x / L, i = threadIdx.x % L;
+    if (threadIdx.x < 32) {
+        const int r = threadIdx.x / 16, i = threadIdx.x % 16;
         const float *cb = r ? p.cb_v : p.cb_k;
-        s_cb[r][i] = cb[i];
-        if (i > 0) codebook_threshold(cb, i, &s_beta[r][i], &s_strict[r][i]);
+        if (i < (r ? LV : LK)) {
+            s_cb[r][i] = cb[i];
+            if (i > 0) codebook_threshold(cb, i, &s_beta[r][i], &s_strict[r][i]);
+        }
     }
     __syncthreads();
 
@@ -282,88 +286,97 @@ paged_encode_kernel(EncodeParams p) {
     float n = sqrt_f64_to_f32_rn((double)ss);
     n = (n < 1e-12f) ? 1e-12f : n;                    // clamp_min(1e-12); NaN passes
 
-    // ---- per-vector thresholds in the x domain ------------------------------
-    const bool finite_n = fabsf(n) < __builtin_inff();
-#pragma unroll
-    for (int i0 = 1; i0 < L; i0 += P) {
-        const int i = i0 + r;
-        if (i < L) {
-            const double beta = s_beta[role][i];
-            double tt = (double)n * beta;             // exact: 24 x 25 significant bits
-            if (s_strict[role][i] && finite_n) tt = next_up(tt);
-            thr[i] = round_up_f32(tt);
+    // ---- thresholds, quantisation, packing and the store, for this role's
+    // codebook (K: LK levels, V: LV levels; wave-uniform branch).
+    auto finish = [&](auto levels) CDA_INLINE {
+        constexpr int L = decltype(levels)::value;
+        constexpr int KB = kD * (L == 16 ? 4 : 2) / 8;   // code bytes of this role
+        // ---- per-vector thresholds in the x domain ------------------------------
+        const bool finite_n = fabsf(n) < __builtin_inff();
+    #pragma unroll
+        for (int i0 = 1; i0 < L; i0 += P) {
+            const int i = i0 + r;
+            if (i < L) {
+                const double beta = s_beta[role][i];
+                double tt = (double)n * beta;             // exact: 24 x 25 significant bits
+                if (s_strict[role][i] && finite_n) tt = next_up(tt);
+                thr[i] = round_up_f32(tt);
+            }
         }
-    }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    ThrVec tv;
-#pragma unroll
-    for (int i = 0; i < 16; ++i) tv[i] = (i >= 1 && i < L) ? thr[i] : 0.0f;
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        ThrVec tv;
+    #pragma unroll
+        for (int i = 0; i < 16; ++i) tv[i] = (i >= 1 && i < L) ? thr[i] : 0.0f;
 
-    // ---- quantise; codes go through LDS (the sq row is free again) ----------
-    uint8_t *idx_row = reinterpret_cast<uint8_t *>(sq_row);
-    uint32_t code[M];
-    if (finite_n) {
-#pragma unroll
-        for (int m = 0; m < M; ++m) code[m] = count_ge<L>(xr[m], tv);
-    } else {
-#pragma unroll
-        for (int m = 0; m < M; ++m) {
-            float u = __fdiv_rn(xr[m], n);
-            u = u < -1.0f ? -1.0f : (u > 1.0f ? 1.0f : u);
-            code[m] = quantize_ref<L>(u, s_cb[role]);
-        }
-    }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();                  // lane sums read before the row is reused
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-#pragma unroll
-    for (int m = 0; m < M; ++m) idx_row[r + P * m] = (uint8_t)code[m];
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-
-    if (!valid) return;
-    const int64_t slot = p.slot_mapping[t];
-    if (slot < 0 || slot >= p.num_slots) return;
-    uint8_t *dst = p.cache + slot * p.row_bytes + (int64_t)h * p.slot_bytes;
-    uint8_t *codes = dst + role * KB;
-    // Lane r packs code bytes [r * KB / P, (r + 1) * KB / P).
-    constexpr int BPL = KB / P;                        // bytes per lane: 16/4 (K4) or 8/2 (K2)
-    constexpr int EPB = L == 16 ? 2 : 4;               // elements per byte
-    const uint32_t *src = reinterpret_cast<const uint32_t *>(idx_row + r * BPL * EPB);
-    uint32_t packed[(BPL + 3) / 4];
-#pragma unroll
-    for (int w = 0; w < (BPL + 3) / 4; ++w) packed[w] = 0;
-#pragma unroll
-    for (int b = 0; b < BPL; ++b) {
-        uint32_t byte;
-        if constexpr (L == 16) {
-            const uint32_t e = src[b / 2] >> (16 * (b & 1));      // elements 2b, 2b+1
-            byte = ((e & 0xFu) << 4) | ((e >> 8) & 0xFu);
+        // ---- quantise; codes go through LDS (the sq row is free again) ----------
+        uint8_t *idx_row = reinterpret_cast<uint8_t *>(sq_row);
+        uint32_t code[M];
+        if (finite_n) {
+    #pragma unroll
+            for (int m = 0; m < M; ++m) code[m] = count_ge<L>(xr[m], tv);
         } else {
-            const uint32_t e = src[b];                           // elements 4b .. 4b+3
-            byte = ((e & 3u) << 6) | (((e >> 8) & 3u) << 4) | (((e >> 16) & 3u) << 2) |
-                   ((e >> 24) & 3u);
+    #pragma unroll
+            for (int m = 0; m < M; ++m) {
+                float u = __fdiv_rn(xr[m], n);
+                u = u < -1.0f ? -1.0f : (u > 1.0f ? 1.0f : u);
+                code[m] = quantize_ref<L>(u, s_cb[role]);
+            }
         }
-        packed[b / 4] |= byte << (8 * (b & 3));
-    }
-    if constexpr (BPL >= 4) {
-#pragma unroll
-        for (int w = 0; w < BPL / 4; ++w)
-            reinterpret_cast<uint32_t *>(codes + r * BPL)[w] = packed[w];
-    } else {
-        *reinterpret_cast<uint16_t *>(codes + r * BPL) = (uint16_t)packed[0];
-    }
-    if (r == 0) *reinterpret_cast<float *>(dst + 2 * KB + 4 * role) = n;
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();                  // lane sums read before the row is reused
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    #pragma unroll
+        for (int m = 0; m < M; ++m) idx_row[r + P * m] = (uint8_t)code[m];
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+        if (!valid) return;
+        const int64_t slot = p.slot_mapping[t];
+        if (slot < 0 || slot >= p.num_slots) return;
+        uint8_t *dst = p.cache + slot * p.row_bytes + (int64_t)h * p.slot_bytes;
+        uint8_t *codes = dst + (role ? KBK : 0);
+        // Lane r packs code bytes [r * KB / P, (r + 1) * KB / P).
+        constexpr int BPL = KB / P;                        // bytes per lane: 16/4 (K4) or 8/2 (K2)
+        constexpr int EPB = L == 16 ? 2 : 4;               // elements per byte
+        const uint32_t *src = reinterpret_cast<const uint32_t *>(idx_row + r * BPL * EPB);
+        uint32_t packed[(BPL + 3) / 4];
+    #pragma unroll
+        for (int w = 0; w < (BPL + 3) / 4; ++w) packed[w] = 0;
+    #pragma unroll
+        for (int b = 0; b < BPL; ++b) {
+            uint32_t byte;
+            if constexpr (L == 16) {
+                const uint32_t e = src[b / 2] >> (16 * (b & 1));      // elements 2b, 2b+1
+                byte = ((e & 0xFu) << 4) | ((e >> 8) & 0xFu);
+            } else {
+                const uint32_t e = src[b];                           // elements 4b .. 4b+3
+                byte = ((e & 3u) << 6) | (((e >> 8) & 3u) << 4) | (((e >> 16) & 3u) << 2) |
+                       ((e >> 24) & 3u);
+            }
+            packed[b / 4] |= byte << (8 * (b & 3));
+        }
+        if constexpr (BPL >= 4) {
+    #pragma unroll
+            for (int w = 0; w < BPL / 4; ++w)
+                reinterpret_cast<uint32_t *>(codes + r * BPL)[w] = packed[w];
+        } else {
+            *reinterpret_cast<uint16_t *>(codes + r * BPL) = (uint16_t)packed[0];
+        }
+        if (r == 0) *reinterpret_cast<float *>(dst + KBK + KBV + 4 * role) = n;
+
+    };
+    if (role == 0) finish(std::integral_constant<int, LK>{});
+    else finish(std::integral_constant<int, LV>{});
 }
 
-template <int L, int P>
+template <int LK, int LV, int P>
 void launch_encode(const EncodeParams &p, int64_t items, hipStream_t st) {
     constexpr int per_block = (64 / P) * kEncWaves / 2;          // items per block
     const int64_t blocks = (items + per_block - 1) / per_block;
-    paged_encode_kernel<L, P><<<dim3((unsigned)blocks), 64 * kEncWaves, 0, st>>>(p);
+    paged_encode_kernel<LK, LV, P><<<dim3((unsigned)blocks), 64 * kEncWaves, 0, st>>>(p);
 }
 
 }  // namespace
@@ -372,24 +385,25 @@ void launch_encode(const EncodeParams &p, int64_t items, hipStream_t st) {
 
 using namespace cda;
 
-extern "C" int cda_paged_encode_fused(const void *k, const void *v, int64_t k_stride,
-                                      int64_t v_stride, const int32_t *slot_mapping,
-                                      int64_t num_tokens, void *flat_cache, int64_t num_slots,
-                                      int slot_bytes, int H_kv, const float *cb_k,
-                                      const float *cb_v, int levels, void *stream) {
-    CDA_REQUIRE(num_tokens >= 0, "cda_paged_encode_fused: num_tokens must be >= 0");
+namespace cda {
+namespace {
+int encode_impl(const void *k, const void *v, int64_t k_stride, int64_t v_stride,
+                const int32_t *slot_mapping, int64_t num_tokens, void *flat_cache,
+                int64_t num_slots, int slot_bytes, int H_kv, const float *cb_k, const float *cb_v,
+                int levels_k, int levels_v, void *stream, const char *fn) {
+    const std::string f(fn);
+    CDA_REQUIRE(num_tokens >= 0, f + ": num_tokens must be >= 0");
     if (num_tokens == 0) return CDA_OK;
-    CDA_REQUIRE(k && v && slot_mapping && flat_cache && cb_k && cb_v,
-                "cda_paged_encode_fused: null pointer argument");
-    CDA_REQUIRE(levels == 16 || levels == 4, "cda_paged_encode_fused: levels must be 16 or 4");
-    CDA_REQUIRE(H_kv > 0 && num_slots > 0, "cda_paged_encode_fused: H_kv and num_slots must be > 0");
-    const int kb = kD * (levels == 16 ? 4 : 2) / 8;
-    CDA_REQUIRE(slot_bytes >= 2 * kb + 8, "cda_paged_encode_fused: slot_bytes too small for the layout");
+    CDA_REQUIRE(k && v && slot_mapping && flat_cache && cb_k && cb_v, f + ": null pointer argument");
+    CDA_REQUIRE(H_kv > 0 && num_slots > 0, f + ": H_kv and num_slots must be > 0");
+    const int kbk = kD * (levels_k == 16 ? 4 : 2) / 8;
+    const int kbv = kD * (levels_v == 16 ? 4 : 2) / 8;
+    CDA_REQUIRE(slot_bytes >= kbk + kbv + 8, f + ": slot_bytes too small for the layout");
     CDA_REQUIRE(k_stride >= (int64_t)H_kv * kD && v_stride >= (int64_t)H_kv * kD,
-                "cda_paged_encode_fused: token stride smaller than H_kv * 128");
+                f + ": token stride smaller than H_kv * 128");
     CDA_REQUIRE(((uintptr_t)k & 3) == 0 && ((uintptr_t)v & 3) == 0 && slot_bytes % 4 == 0 &&
                     ((uintptr_t)flat_cache & 3) == 0,
-                "cda_paged_encode_fused: k, v, cache must be 4-byte aligned");
+                f + ": k, v, cache must be 4-byte aligned");
     EncodeParams p;
     p.k = static_cast<const uint16_t *>(k);
     p.v = static_cast<const uint16_t *>(v);
@@ -405,17 +419,41 @@ extern "C" int cda_paged_encode_fused(const void *k, const void *v, int64_t k_st
     p.cb_k = cb_k;
     p.cb_v = cb_v;
     const int64_t items = num_tokens * H_kv;
-    CDA_REQUIRE(items < ((int64_t)1 << 31), "cda_paged_encode_fused: too many tokens x heads");
+    CDA_REQUIRE(items < ((int64_t)1 << 31), f + ": too many tokens x heads");
     hipStream_t st = static_cast<hipStream_t>(stream);
     // Four lanes per vector run the fewest instructions per vector; sixteen
     // finish a wave four times sooner.  Take 16 while the 4-lane grid would
     // leave the SIMDs with fewer than two waves each.
     const bool wide = items * 2 / 16 < 2048;
-    if (levels == 16) {
-        if (wide) launch_encode<16, 16>(p, items, st); else launch_encode<16, 4>(p, items, st);
+    if (levels_k == 16 && levels_v == 16) {
+        if (wide) launch_encode<16, 16, 16>(p, items, st); else launch_encode<16, 16, 4>(p, items, st);
+    } else if (levels_k == 4 && levels_v == 4) {
+        if (wide) launch_encode<4, 4, 16>(p, items, st); else launch_encode<4, 4, 4>(p, items, st);
     } else {
-        if (wide) launch_encode<4, 16>(p, items, st); else launch_encode<4, 4>(p, items, st);
+        if (wide) launch_encode<16, 4, 16>(p, items, st); else launch_encode<16, 4, 4>(p, items, st);
     }
-    CDA_LAUNCH_CHECK("paged_encode_kernel");
+    CDA_LAUNCH_CHECK(f + ": paged_encode_kernel");
     return CDA_OK;
+}
+}  // namespace
+}  // namespace cda
+
+extern "C" int cda_paged_encode_fused(const void *k, const void *v, int64_t k_stride,
+                                      int64_t v_stride, const int32_t *slot_mapping,
+                                      int64_t num_tokens, void *flat_cache, int64_t num_slots,
+                                      int slot_bytes, int H_kv, const float *cb_k,
+                                      const float *cb_v, int levels, void *stream) {
+    CDA_REQUIRE(levels == 16 || levels == 4, "cda_paged_encode_fused: levels must be 16 or 4");
+    return encode_impl(k, v, k_stride, v_stride, slot_mapping, num_tokens, flat_cache, num_slots,
+                       slot_bytes, H_kv, cb_k, cb_v, levels, levels, stream,
+                       "cda_paged_encode_fused");
+}
+
+extern "C" int cda_paged_encode_fused_k4v2(const void *k, const void *v, int64_t k_stride,
+                                           int64_t v_stride, const int32_t *slot_mapping,
+                                           int64_t num_tokens, void *flat_cache,
+                                           int64_t num_slots, int slot_bytes, int H_kv,
+                                           const float *cb_k, const float *cb_v, void *stream) {
+    return encode_impl(k, v, k_stride, v_stride, slot_mapping, num_tokens, flat_cache, num_slots,
+                       slot_bytes, H_kv, cb_k, cb_v, 16, 4, stream, "cda_paged_encode_fused_k4v2");
 }

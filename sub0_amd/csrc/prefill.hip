@@ -279,6 +279,15 @@ __device__ __forceinline__ uint32_t dq_byte(const uint8_t *lut, uint32_t byte, f
     return cvt_pk(c.x * norm, c.y * norm);
 }
 
+// fp16(cb[a] * norm), fp16(cb[b] * norm) packed, from a table of 64 lane
+// columns (row = code).
+__device__ __forceinline__ uint32_t dq_codes(const uint8_t *lut, uint32_t a, uint32_t b,
+                                            uint32_t col, float norm) {
+    const float x = *reinterpret_cast<const float *>(lut + (a << 8) + col);
+    const float y = *reinterpret_cast<const float *>(lut + (b << 8) + col);
+    return cvt_pk(x * norm, y * norm);
+}
+
 __device__ __forceinline__ uint32_t dq_pair(const uint8_t *lut, uint32_t byte, uint32_t col,
                                            float norm) {
     const float hi = *reinterpret_cast<const float *>(lut + ((byte >> 4) << 8) + col);
@@ -628,6 +637,7 @@ prefill_kernel(PrefillParams p) {
 // of (B*max_seq, H_kv, 128) fp16 = fp16(centroid * norm) for t < seq_lens[b],
 // zeros beyond.  One 256-thread block per (4 rows of one sequence); thread =
 // (row, head, 16-dim chunk); the per-code tables sit in LDS (64 lane columns).
+template <int LV>
 __global__ void __launch_bounds__(256)
 paged_to_dense_kernel(const uint8_t *kv, int64_t row_bytes, int slot_bytes, int H_kv,
                       const int32_t *block_table, int bt_stride, const int32_t *seq_lens,
@@ -636,7 +646,8 @@ paged_to_dense_kernel(const uint8_t *kv, int64_t row_bytes, int slot_bytes, int 
     __shared__ float lut[2][16 * 64];
     const int tid = threadIdx.x;
     for (int i = tid; i < 2 * 16 * 64; i += 256)
-        lut[i >> 10][i & 1023] = (i < 1024) ? cb_k[(i & 1023) >> 6] : cb_v[(i & 1023) >> 6];
+        lut[i >> 10][i & 1023] = (i < 1024) ? cb_k[(i & 1023) >> 6]
+                                            : (((i & 1023) >> 6) < LV ? cb_v[(i & 1023) >> 6] : 0.0f);
     __syncthreads();
     const int b = blockIdx.y;
     const int n = min(seq_lens[b], bt_stride * block_size);
@@ -653,17 +664,33 @@ paged_to_dense_kernel(const uint8_t *kv, int64_t row_bytes, int slot_bytes, int 
             const int64_t slot =
                 (int64_t)block_table[(int64_t)b * bt_stride + t / block_size] * block_size + t % block_size;
             const uint8_t *rp = kv + slot * row_bytes + (int64_t)h * slot_bytes;
+            // Slot: [K codes 64 | V codes KBV | K norm | V norm].
+            constexpr int KBV = LV == 16 ? 64 : 32;
             const uint2 kc = *reinterpret_cast<const uint2 *>(rp + 8 * c);
-            const uint2 vc = *reinterpret_cast<const uint2 *>(rp + 64 + 8 * c);
-            const float nk = *reinterpret_cast<const float *>(rp + 128);
-            const float nv = *reinterpret_cast<const float *>(rp + 132);
+            const float nk = *reinterpret_cast<const float *>(rp + 64 + KBV);
+            const float nv = *reinterpret_cast<const float *>(rp + 68 + KBV);
             uint32_t kw[8], vw[8];
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
                 const uint32_t kb = ((j < 4 ? kc.x : kc.y) >> (8 * (j & 3))) & 0xFFu;
-                const uint32_t vb = ((j < 4 ? vc.x : vc.y) >> (8 * (j & 3))) & 0xFFu;
                 kw[j] = dq_pair(lk, kb, col, nk);
-                vw[j] = dq_pair(lv, vb, col, nv);
+            }
+            if constexpr (LV == 16) {
+                const uint2 vc = *reinterpret_cast<const uint2 *>(rp + 64 + 8 * c);
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const uint32_t vb = ((j < 4 ? vc.x : vc.y) >> (8 * (j & 3))) & 0xFFu;
+                    vw[j] = dq_pair(lv, vb, col, nv);
+                }
+            } else {
+                // 2-bit codes: dim 4j at bits 7:6 of byte j (compression.py:382-386).
+                const uint32_t vc = *reinterpret_cast<const uint32_t *>(rp + 64 + 4 * c);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const uint32_t vb = (vc >> (8 * j)) & 0xFFu;
+                    vw[2 * j] = dq_codes(lv, vb >> 6, (vb >> 4) & 3u, col, nv);
+                    vw[2 * j + 1] = dq_codes(lv, (vb >> 2) & 3u, vb & 3u, col, nv);
+                }
             }
             ko0 = make_uint4(kw[0], kw[1], kw[2], kw[3]);
             ko1 = make_uint4(kw[4], kw[5], kw[6], kw[7]);
@@ -1115,6 +1142,45 @@ extern "C" int cda_dequantize_rows(const void *codes, const float *norms, int64_
     return CDA_OK;
 }
 
+namespace cda {
+namespace {
+int paged_to_dense_impl(const void *kv_cache, int slot_bytes, int H_kv, const int32_t *block_table,
+                        int bt_stride, const int32_t *seq_lens, int B, const float *cb_k,
+                        const float *cb_v, int levels_v, int block_size, int max_seq_len,
+                        void *k_out, void *v_out, void *stream, const char *fn) {
+    const std::string f(fn);
+    CDA_REQUIRE(kv_cache && block_table && seq_lens && cb_k && cb_v && k_out && v_out,
+                f + ": null pointer argument");
+    CDA_REQUIRE(B >= 0 && H_kv > 0 && max_seq_len >= 0 && block_size > 0 && bt_stride > 0,
+                f + ": bad shape arguments");
+    const int data = 64 + (levels_v == 16 ? 64 : 32) + 8;
+    CDA_REQUIRE(slot_bytes >= data && slot_bytes % 8 == 0,
+                f + ": slot too small for the layout (136 B K4V4, 104 B K4V2) or not a "
+                    "multiple of 8");
+    CDA_REQUIRE(((uintptr_t)kv_cache & 7) == 0 && ((uintptr_t)k_out & 15) == 0 &&
+                    ((uintptr_t)v_out & 15) == 0,
+                f + ": misaligned pointer");
+    if (B == 0 || max_seq_len == 0) return CDA_OK;
+    const dim3 grid((max_seq_len + 3) / 4, B);
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    const auto *kv = static_cast<const uint8_t *>(kv_cache);
+    const int64_t row = (int64_t)H_kv * slot_bytes;
+    auto *ko = static_cast<uint16_t *>(k_out);
+    auto *vo = static_cast<uint16_t *>(v_out);
+    if (levels_v == 16)
+        paged_to_dense_kernel<16><<<grid, 256, 0, st>>>(kv, row, slot_bytes, H_kv, block_table,
+                                                        bt_stride, seq_lens, cb_k, cb_v,
+                                                        block_size, max_seq_len, ko, vo);
+    else
+        paged_to_dense_kernel<4><<<grid, 256, 0, st>>>(kv, row, slot_bytes, H_kv, block_table,
+                                                       bt_stride, seq_lens, cb_k, cb_v,
+                                                       block_size, max_seq_len, ko, vo);
+    CDA_LAUNCH_CHECK(f + ": paged_to_dense_kernel");
+    return CDA_OK;
+}
+}  // namespace
+}  // namespace cda
+
 extern "C" int cda_fa2_paged_cache_to_dense_rotated(const void *kv_cache, int64_t num_slots,
                                                     int slot_bytes, int H_kv,
                                                     const int32_t *block_table, int bt_stride,
@@ -1123,23 +1189,20 @@ extern "C" int cda_fa2_paged_cache_to_dense_rotated(const void *kv_cache, int64_
                                                     int levels, int block_size, int max_seq_len,
                                                     void *k_out, void *v_out, void *stream) {
     (void)num_slots;
-    CDA_REQUIRE(kv_cache && block_table && seq_lens && cb_k && cb_v && k_out && v_out,
-                "cda_fa2_paged_cache_to_dense_rotated: null pointer argument");
-    CDA_REQUIRE(B >= 0 && H_kv > 0 && max_seq_len >= 0 && block_size > 0 && bt_stride > 0,
-                "cda_fa2_paged_cache_to_dense_rotated: bad shape arguments");
-    CDA_REQUIRE(levels == 16 && slot_bytes >= 136 && slot_bytes % 8 == 0,
-                "cda_fa2_paged_cache_to_dense_rotated: K4V4 caches only (16 levels, slot >= 136 B)");
-    CDA_REQUIRE(((uintptr_t)kv_cache & 7) == 0 && ((uintptr_t)k_out & 15) == 0 &&
-                    ((uintptr_t)v_out & 15) == 0,
-                "cda_fa2_paged_cache_to_dense_rotated: misaligned pointer");
-    if (B == 0 || max_seq_len == 0) return CDA_OK;
-    const dim3 grid((max_seq_len + 3) / 4, B);
-    paged_to_dense_kernel<<<grid, 256, 0, static_cast<hipStream_t>(stream)>>>(
-        static_cast<const uint8_t *>(kv_cache), (int64_t)H_kv * slot_bytes, slot_bytes, H_kv,
-        block_table, bt_stride, seq_lens, cb_k, cb_v, block_size, max_seq_len,
-        static_cast<uint16_t *>(k_out), static_cast<uint16_t *>(v_out));
-    CDA_LAUNCH_CHECK("paged_to_dense_kernel");
-    return CDA_OK;
+    CDA_REQUIRE(levels == 16, "cda_fa2_paged_cache_to_dense_rotated: K4V4 caches only (16 levels)");
+    return paged_to_dense_impl(kv_cache, slot_bytes, H_kv, block_table, bt_stride, seq_lens, B,
+                               cb_k, cb_v, 16, block_size, max_seq_len, k_out, v_out, stream,
+                               "cda_fa2_paged_cache_to_dense_rotated");
+}
+
+extern "C" int cda_fa2_paged_cache_to_dense_rotated_k4v2(
+    const void *kv_cache, int64_t num_slots, int slot_bytes, int H_kv, const int32_t *block_table,
+    int bt_stride, const int32_t *seq_lens, int B, const float *cb_k, const float *cb_v,
+    int block_size, int max_seq_len, void *k_out, void *v_out, void *stream) {
+    (void)num_slots;
+    return paged_to_dense_impl(kv_cache, slot_bytes, H_kv, block_table, bt_stride, seq_lens, B,
+                               cb_k, cb_v, 4, block_size, max_seq_len, k_out, v_out, stream,
+                               "cda_fa2_paged_cache_to_dense_rotated_k4v2");
 }
 
 extern "C" int cda_hadamard128_fp16(const void *x, void *y, int64_t rows, float scale,

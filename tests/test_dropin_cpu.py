@@ -25,8 +25,9 @@ def test_loader_names_and_errors():
     assert H.load_decode_hmma(group_size=8) is load_pybind_module("_v1_decode_hmma_k4v4_gs8")
     with pytest.raises(ValueError):
         H.load_decode_hmma(group_size=2)
-    with pytest.raises(PrebuiltMissing):
-        H.load_kv_cache_update()
+    assert callable(H.load_kv_cache_update(k4v2=True).cda_paged_encode_fused)
+    assert callable(H.load_decode_hmma(k4v2=True, group_size=4).cda_decode_full_hmma_v3)
+    assert callable(H.load_fa2_cda_loader(k4v2=True).cda_fa2_paged_cache_to_dense_rotated)
     with pytest.raises(PrebuiltMissing):
         load_pybind_module("no_such_kernel")
     assert issubclass(PrebuiltMissing, ImportError)

@@ -169,6 +169,37 @@ def test_decode_matches_fp64_textbook_attention():
             np.testing.assert_allclose(out[b, hq], ref, atol=1e-3, rtol=0)
 
 
+def test_k4v2_layout_decode_matches_fp64_textbook_attention(codebooks):
+    """The legacy K4V2 slot (104 B: K 4-bit | V 2-bit | K norm | V norm,
+    cda_attn_v2.py:29): the paged decode reads the fields at those offsets and
+    decodes V with the 4-level codebook; checked by brute force as above."""
+    cbk, cbv = codebooks["lloyd_beta16"], codebooks["lloyd_beta4"]
+    B, H_kv, gs, bs, N = 2, 2, 4, 16, 90
+    k = synth.kv_with_outliers(31, (B, H_kv, N, D))
+    v = synth.normal_f16(32, (B, H_kv, N, D))
+    q = synth.normal_f16(33, (B, H_kv * gs, D))
+    kp, kn, _ = O.encode(k, cbk)
+    vp, vn, _ = O.encode(v, cbv)
+    W = (N + bs - 1) // bs
+    bt = synth.permuted_block_table(34, B, W)
+    cache = O.build_paged_cache(kp, kn, vp, vn, bt, bs, 16, num_blocks=B * W, Lv=4)
+    assert cache.shape[-1] == 104
+    sl = np.array([N, 41], np.int32)
+    R = O.hadamard128().astype(np.float64)
+    out = O.decode_paged(q, cache, bt, sl, cbk, cbv, O.hadamard128(), H_kv=H_kv,
+                         block_size=bs).astype(np.float64)
+    for b, n in enumerate(sl):
+        for hq in range(H_kv * gs):
+            h = hq // gs
+            K = O.decode_rotated(kp[b, h, :n], kn[b, h, :n], cbk).astype(np.float64)
+            V = O.decode_rotated(vp[b, h, :n], vn[b, h, :n], cbv).astype(np.float64)
+            qr = (q[b, hq].astype(np.float64) @ R).astype(np.float32).astype(np.float16)
+            s_ = K @ qr.astype(np.float64) / math.sqrt(D)
+            p = np.exp(s_ - s_.max())
+            orot = ((p @ V) / p.sum()).astype(np.float32).astype(np.float16).astype(np.float64)
+            np.testing.assert_allclose(out[b, hq], orot @ R.T, atol=1e-3, rtol=0)
+
+
 def test_split_merge_equals_single_pass():
     c = _case(22, [203])
     R = O.hadamard128()
