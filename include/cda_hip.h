@@ -206,6 +206,39 @@ int cda_prefill_paged_hadamard_ws(const void *q, const void *kv_cache, int64_t n
                                   int block_size, int max_query_len, int max_seq_len, float scale,
                                   void *workspace, size_t workspace_bytes, void *stream);
 
+/* Replaces the reference's hybrid chunked prefill
+ *   hybrid_attn_v1(q, k, v, output, kv_cache_flat, block_table, cu_seqlens_q=,
+ *                  seq_lens=, cb_K=, cb_V=, rotation_fp32=, rotation_fp16=,
+ *                  scale=, group_size=, block_size=)
+ * called by cda/kernels_cuda/vllm_integration/cda_attn_v2.py:1023-1060 and
+ * :1474-1532 (CDA_PREFILL_BACKEND fa2_rawkv / fa2_cda_rawkv /
+ * fa2_cda_fused_rawkv with a compressed prefix; the reference's own wrapper was
+ * removed, wrappers.py:14-20).  Sequence b's queries are the last
+ * q_len = cu_seqlens_q[b+1] - cu_seqlens_q[b] of its seq_lens[b] positions.
+ * They attend to keys [0, seq_lens[b] - q_len) of the compressed cache (all
+ * visible) and to the chunk's own fresh keys k_new / v_new rows
+ * [cu_seqlens_q[b], cu_seqlens_q[b+1]) (causal), in one softmax: the chunk's K
+ * and V are rotated to fp16(x H / sqrt(128)) (fa2_cda.py:256-287), each source
+ * writes split partials (O, m, l), and the merge (attention.py:239-272) rounds
+ * O_rot to fp16 and applies the inverse rotation.
+ *   q, out:         (T, H_q, 128) fp16, unrotated
+ *   k_new, v_new:   (T, H_kv, 128) fp16, unrotated, contiguous
+ *   kv_cache:       K4V4 paged cache (levels 16)
+ *   max_seq_len:    upper bound of seq_lens (plans the splits only)
+ *   workspace:      256-byte aligned device scratch of at least
+ *                   cda_prefill_hybrid_workspace_size(...) bytes
+ * Calls sharing one workspace must not overlap.
+ */
+size_t cda_prefill_hybrid_workspace_size(int B, int T, int H_q, int H_kv, int max_query_len,
+                                         int max_seq_len);
+int cda_prefill_hybrid_rawkv(const void *q, const void *k_new, const void *v_new,
+                             const void *kv_cache, int64_t num_slots, int slot_bytes, int H_kv,
+                             const int32_t *block_table, int bt_stride,
+                             const int32_t *cu_seqlens_q, const int32_t *seq_lens, int B,
+                             const float *cb_k, const float *cb_v, int levels, void *out, int T,
+                             int H_q, int block_size, int max_query_len, int max_seq_len,
+                             float scale, void *workspace, size_t workspace_bytes, void *stream);
+
 /* Replaces the reference pybind function
  *   cda_fa2_varlen_fwd_hadamard(Q, k_rot, v_rot, out, cu_q, cu_k, seqused_k,
  *                               max_q, max_k, scale)      (causal only)

@@ -8,6 +8,9 @@ need no arithmetic contract:
   (``cda/algorithm/compression.py:163-188, 375-397``);
 * ``uniform_centroids`` (``compression.py:75-83``);
 * ``merge_partials`` (``cda/algorithm/attention.py:239-272``);
+* ``hybrid_prefill``: chunked prefill over a compressed prefix plus the
+  chunk's raw K/V, merged by ``merge_partials`` (the contract of
+  ``cda/kernels_cuda/vllm_integration/cda_attn_v2.py:1023-1060``);
 * ``build_paged_cache``: scatters encoded rows into the paged slot layout of
   ``cda/kernels_cuda/vllm_integration/cda_attn_v2.py:20-27`` (K codes | V codes
   | K norm fp32 | V norm fp32 | pad).
@@ -269,3 +272,73 @@ def merge_partials(partials):
     lg = (ls * corr).sum(axis=0)
     O = (Os * corr[..., None]).sum(axis=0) / np.maximum(lg, 1e-30)[..., None]
     return O.astype(np.float16)
+
+
+def paged_rows(cache, block_table, b, n, cbK, cbV, *, H_kv, block_size):
+    """Rotated-frame fp16 K, V rows (H_kv, n, 128) of sequence b's first n
+    keys, decoded from the paged cache (compression.py:337-361)."""
+    cbK = np.asarray(cbK, dtype=np.float32)
+    cbV = np.asarray(cbV, dtype=np.float32)
+    kb, _ = slot_layout(cbK.size)
+    kbv = slot_layout(cbV.size)[0]
+    t = np.arange(n)
+    rows = block_table[b, t // block_size].astype(np.int64) * block_size + t % block_size
+    slots = cache[rows]                                          # (n, H_kv, slot)
+    kn = np.ascontiguousarray(slots[:, :, kb + kbv:kb + kbv + 4]).view(np.float32)[..., 0]
+    vn = np.ascontiguousarray(slots[:, :, kb + kbv + 4:kb + kbv + 8]).view(np.float32)[..., 0]
+    k = decode_rotated(np.ascontiguousarray(slots[:, :, :kb].transpose(1, 0, 2)),
+                       np.ascontiguousarray(kn.T), cbK)
+    v = decode_rotated(np.ascontiguousarray(slots[:, :, kb:kb + kbv].transpose(1, 0, 2)),
+                       np.ascontiguousarray(vn.T), cbV)
+    return k, v
+
+
+def _partial(q_rot, k, v, scale, mask=None):
+    """attention_partial_reference (attention.py:190-236) in float64 for one
+    (query rows, keys) block: (O_unnorm, m, l) with m in the natural domain."""
+    s = (q_rot.astype(np.float64) @ k.astype(np.float64).T) * scale
+    if mask is not None:
+        s = np.where(mask, s, -np.inf)
+    m = s.max(axis=-1) if s.shape[-1] else np.full(s.shape[0], -np.inf)
+    with np.errstate(invalid="ignore"):
+        p = np.exp(s - m[:, None])
+    p = np.where(np.isnan(p), 0.0, p)
+    return p @ v.astype(np.float64), m, p.sum(axis=-1)
+
+
+def hybrid_prefill(q, cu_q, k_new, v_new, cache, block_table, seq_lens, cbK, cbV, R, *,
+                   H_kv, block_size, scale=None):
+    """Chunked prefill with a compressed prefix (cda_attn_v2.py:1023-1060):
+    sequence b's queries (the last q_len of its seq_lens[b] positions) attend
+    to keys [0, seq_lens[b] - q_len) decoded from the cache (all visible) and
+    to the chunk's own K/V rotated to fp16(x R) (fa2_cda.py:256-287; causal),
+    the two partials merged by merge_partials (attention.py:239-272), then
+    out = fp16(fp16(O_rot) R^T).  q (T, H_q, 128), k_new/v_new (T, H_kv, 128)
+    fp16; returns (T, H_q, 128) fp16."""
+    q = np.asarray(q, dtype=np.float16)
+    T, H_q, _ = q.shape
+    gs = H_q // H_kv
+    R32 = np.asarray(R, dtype=np.float32)
+    if scale is None:
+        scale = 1.0 / np.sqrt(D)
+    q_rot = (q.astype(np.float32) @ R32).astype(np.float16)
+    k_rot = (np.asarray(k_new, dtype=np.float16).astype(np.float32) @ R32).astype(np.float16)
+    v_rot = (np.asarray(v_new, dtype=np.float16).astype(np.float32) @ R32).astype(np.float16)
+    out = np.zeros((T, H_q, D), dtype=np.float16)
+    for b in range(len(cu_q) - 1):
+        q0, q1 = int(cu_q[b]), int(cu_q[b + 1])
+        n = q1 - q0
+        if n == 0:
+            continue
+        past = int(seq_lens[b]) - n
+        kp, vp = paged_rows(cache, block_table, b, past, cbK, cbV, H_kv=H_kv,
+                            block_size=block_size)
+        causal = np.arange(n)[None, :] <= np.arange(n)[:, None]
+        for hq in range(H_q):
+            h = hq // gs
+            qr = q_rot[q0:q1, hq]
+            parts = [_partial(qr, kp[h], vp[h], scale),
+                     _partial(qr, k_rot[q0:q1, h], v_rot[q0:q1, h], scale, causal)]
+            o_rot = merge_partials(parts)
+            out[q0:q1, hq] = (o_rot.astype(np.float32) @ R32.T).astype(np.float16)
+    return out

@@ -42,6 +42,8 @@ SYMBOLS = (
     "cda_dequantize_rows",
     "cda_fa2_paged_cache_to_dense_rotated",
     "cda_hadamard128_fp16",
+    "cda_prefill_hybrid_workspace_size",
+    "cda_prefill_hybrid_rawkv",
 )
 
 
@@ -122,6 +124,12 @@ def lib():
         L.cda_prefill_paged_hadamard_ws.argtypes = [
             _P, _P, _I64, _I32, _I32, _P, _I32, _P, _P, _I32, _P, _P, _I32, _P, _I32, _I32,
             _I32, _I32, _I32, _F32, _P, _SZ, _P]
+        L.cda_prefill_hybrid_workspace_size.restype = _SZ
+        L.cda_prefill_hybrid_workspace_size.argtypes = [_I32, _I32, _I32, _I32, _I32, _I32]
+        L.cda_prefill_hybrid_rawkv.restype = _I32
+        L.cda_prefill_hybrid_rawkv.argtypes = [
+            _P, _P, _P, _P, _I64, _I32, _I32, _P, _I32, _P, _P, _I32, _P, _P, _I32, _P, _I32,
+            _I32, _I32, _I32, _I32, _F32, _P, _SZ, _P]
         L.cda_fa2_varlen_fwd_hadamard.restype = _I32
         L.cda_fa2_varlen_fwd_hadamard.argtypes = [
             _P, _P, _P, _P, _P, _P, _P, _I32, _I32, _I32, _I32, _I32, _I32, _F32, _P]
@@ -381,6 +389,59 @@ def prefill_workspace_size(B: int, T: int, H_q: int, H_kv: int, max_query_len: i
                            max_seq_len: int) -> int:
     """Bytes of scratch the key-split prefill needs (0: it would not split)."""
     return int(lib().cda_prefill_workspace_size(B, T, H_q, H_kv, max_query_len, max_seq_len))
+
+
+def prefill_hybrid(q: torch.Tensor, k_new: torch.Tensor, v_new: torch.Tensor,
+                   kv_cache: torch.Tensor, block_table: torch.Tensor,
+                   cu_seqlens_q: torch.Tensor, seq_lens: torch.Tensor, cb_k: torch.Tensor,
+                   cb_v: torch.Tensor, out: torch.Tensor, *, block_size: int,
+                   max_query_len: int, max_seq_len: int, scale: float,
+                   workspace: torch.Tensor | None = None) -> None:
+    """Chunked prefill over a compressed prefix plus the chunk's own fresh K/V
+    (``cda_prefill_hybrid_rawkv``): the queries of sequence b are the last
+    ``cu_seqlens_q[b+1] - cu_seqlens_q[b]`` of its ``seq_lens[b]`` positions;
+    keys before the chunk come from the paged cache, the chunk's keys from
+    ``k_new`` / ``v_new`` (T, H_kv, 128) fp16 (unrotated, causal), merged by
+    log-sum-exp.  ``out`` (T, H_q, 128) fp16 is written in place."""
+    dev = _require_gpu(q, k_new, v_new, kv_cache, block_table, cu_seqlens_q, seq_lens, cb_k,
+                       cb_v, out)
+    for t, nm in ((q, "Q"), (k_new, "K"), (v_new, "V"), (out, "output")):
+        if t.dtype != torch.float16:
+            raise TypeError(f"{nm} must be fp16")
+        if t.dim() != 3 or t.shape[-1] != 128 or not t.is_contiguous():
+            raise ValueError(f"{nm} must be a contiguous (T, heads, 128) tensor")
+    if out.shape != q.shape:
+        raise ValueError("output must be shaped like Q")
+    if k_new.shape != v_new.shape or k_new.shape[0] != q.shape[0]:
+        raise ValueError("K and V must be (T, H_kv, 128) with the T of Q")
+    if cu_seqlens_q.dtype != torch.int32:
+        raise TypeError("cu_seqlens_q must be int32")
+    _check_paged(kv_cache, block_table, seq_lens, cb_k, cb_v)
+    T, H_q, _ = q.shape
+    B = cu_seqlens_q.numel() - 1
+    if seq_lens.numel() < B or block_table.shape[0] < B:
+        raise ValueError("seq_lens / block_table have fewer rows than cu_seqlens_q")
+    num_slots, H_kv, slot_bytes = kv_cache.shape
+    if k_new.shape[1] != H_kv:
+        raise ValueError(f"K/V have {k_new.shape[1]} heads, the cache {H_kv}")
+    if B == 0 or T == 0 or max_query_len <= 0:
+        return
+    need = int(lib().cda_prefill_hybrid_workspace_size(B, T, H_q, H_kv, int(max_query_len),
+                                                        max(1, int(max_seq_len))))
+    if need == 0:
+        raise ValueError("unsupported hybrid prefill shape (H_q / H_kv must be 4 or 8)")
+    if (workspace is None or workspace.device != dev
+            or workspace.numel() - ((-workspace.data_ptr()) % 256) < need):
+        workspace = torch.empty(need + 256, dtype=torch.uint8, device=dev)
+    ws_ptr = workspace.data_ptr()
+    pad = (-ws_ptr) % 256
+    rc = lib().cda_prefill_hybrid_rawkv(
+        _ptr(q), _ptr(k_new), _ptr(v_new), _ptr(kv_cache), num_slots, slot_bytes, H_kv,
+        _ptr(block_table), block_table.stride(0), _ptr(cu_seqlens_q), _ptr(seq_lens), B,
+        _ptr(cb_k.float().contiguous()), _ptr(cb_v.float().contiguous()), 16, _ptr(out), T, H_q,
+        int(block_size), int(max_query_len), int(max_seq_len), float(scale),
+        ctypes.c_void_p(ws_ptr + pad), workspace.numel() - pad, _stream(dev))
+    _check(rc, "cda_prefill_hybrid_rawkv")
 
 
 def fa2_varlen_fwd_hadamard(q: torch.Tensor, k_rot: torch.Tensor, v_rot: torch.Tensor,

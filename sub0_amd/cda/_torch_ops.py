@@ -9,7 +9,8 @@ implementations that call the C ABI of ``libcda_hip.so`` through
 ``torch.ops.cda_hip`` -- the product entry points the reference reaches
 through its pybind modules (``cda/kernels_cuda/wrappers.py:115-124,
 153-156``, ``fa2_cda.py:51-52, 85-95, 166-181``): ``decode``, ``encode``,
-``prefill``, ``paged_to_dense``, ``varlen_fwd_hadamard``, ``hadamard128``.
+``prefill``, ``prefill_hybrid``, ``paged_to_dense``, ``varlen_fwd_hadamard``,
+``varlen_fwd``, ``hadamard128``.
 ``load_pybind_module`` routes its module functions through these ops.
 
 ``torch.ops._cda_vllm_fa2_fork_C`` -- the comparator namespace of the
@@ -61,6 +62,17 @@ def _prefill(q, kv_cache, block_table, cu_seqlens_q, seq_lens, cb_k, cb_v, out, 
                           max_seq_len=None if max_seq_len < 0 else max_seq_len)
 
 
+def _prefill_hybrid(q, k_new, v_new, kv_cache, block_table, cu_seqlens_q, seq_lens, cb_k,
+                    cb_v, out, block_size, max_query_len, max_seq_len, scale):
+    _native.prefill_hybrid(q, k_new, v_new, kv_cache, block_table, cu_seqlens_q, seq_lens, cb_k,
+                           cb_v, out, block_size=block_size, max_query_len=max_query_len,
+                           max_seq_len=max_seq_len, scale=scale)
+
+
+def _varlen_fwd_plain(q, k, v, out, cu_q, cu_k, seqused_k, max_q, scale, causal):
+    _native.fa2_varlen_fwd(q, k, v, out, cu_q, cu_k, seqused_k, max_q, scale, causal)
+
+
 def _paged_to_dense(kv_cache, block_table, seq_lens, cb_k, cb_v, block_size, max_seq_len):
     return _native.paged_to_dense(kv_cache, block_table, seq_lens, cb_k, cb_v,
                                   block_size=block_size, max_seq_len=max_seq_len)
@@ -96,6 +108,13 @@ _define(_cda, "encode(Tensor k, Tensor v, Tensor slot_mapping, Tensor(a!) flat_c
 _define(_cda, "prefill(Tensor q, Tensor kv_cache, Tensor block_table, Tensor cu_seqlens_q, "
               "Tensor seq_lens, Tensor cb_k, Tensor cb_v, Tensor(a!) out, int block_size, "
               "int max_query_len, float scale, int max_seq_len=-1) -> ()", _prefill, _nothing)
+_define(_cda, "prefill_hybrid(Tensor q, Tensor k_new, Tensor v_new, Tensor kv_cache, "
+              "Tensor block_table, Tensor cu_seqlens_q, Tensor seq_lens, Tensor cb_k, "
+              "Tensor cb_v, Tensor(a!) out, int block_size, int max_query_len, "
+              "int max_seq_len, float scale) -> ()", _prefill_hybrid, _nothing)
+_define(_cda, "varlen_fwd(Tensor q, Tensor k, Tensor v, Tensor(a!) out, Tensor cu_seqlens_q, "
+              "Tensor cu_seqlens_k, Tensor seqused_k, int max_seqlen_q, float scale, "
+              "bool causal) -> ()", _varlen_fwd_plain, _nothing)
 _define(_cda, "paged_to_dense(Tensor kv_cache, Tensor block_table, Tensor seq_lens, "
               "Tensor cb_k, Tensor cb_v, int block_size, int max_seq_len) -> (Tensor, Tensor)",
         _paged_to_dense, _paged_to_dense_fake)

@@ -34,6 +34,7 @@ import torch
 from torch import Tensor
 
 from sub0_amd import _native
+from sub0_amd.cda import _torch_ops  # noqa: F401  -- registers torch.ops.cda_hip
 from sub0_amd.cda.kernels_cuda.hmma_loader import (
     load_fa2_cda_hadamard,
     load_fa2_cda_loader,
@@ -132,8 +133,6 @@ def fa2_cda_prefill_varlen_v1(
         raise ValueError("H_q must be divisible by group_size")
     if not causal:
         raise NotImplementedError("the MI355X prefill kernels are causal-only")
-    if k4v2:
-        load_fa2_cda_loader(k4v2=True)   # raises PrebuiltMissing: no K4V2 build
     if scale is None:
         scale = 1.0 / math.sqrt(D)
     cu_q = cu_seqlens_q.to(torch.int32) if cu_seqlens_q.dtype != torch.int32 else cu_seqlens_q
@@ -141,12 +140,14 @@ def fa2_cda_prefill_varlen_v1(
     bt = block_table.to(torch.int32) if block_table.dtype != torch.int32 else block_table
     kv = kv_cache.view(-1, *kv_cache.shape[-2:]) if kv_cache.dim() == 4 else kv_cache
     out = output if output.is_contiguous() else torch.empty_like(output)
-    dense = return_dense_kv or prefill_source(B, kv.shape[-2], int(max_query_len),
-                                              int(max_seq_len)) == "dense"
+    # K4V2 caches are read through the dense bridge (the compressed-tile
+    # kernel reads K4V4 slots).
+    dense = return_dense_kv or k4v2 or prefill_source(B, kv.shape[-2], int(max_query_len),
+                                                      int(max_seq_len)) == "dense"
     if dense:
         k_rot, v_rot = paged_cache_to_dense_rotated(kv, bt, sl, cb_K=cb_K, cb_V=cb_V,
                                                     block_size=block_size,
-                                                    max_seq_len=max_seq_len)
+                                                    max_seq_len=max_seq_len, k4v2=k4v2)
         cu_k = torch.arange(0, B + 1, dtype=torch.int32, device=Q_in.device) * int(max_seq_len)
         load_fa2_cda_varlen_fused().cda_fa2_varlen_fwd_hadamard(
             Q_in.contiguous(), k_rot, v_rot, out, cu_q.contiguous(), cu_k, sl.contiguous(),
@@ -162,3 +163,118 @@ def fa2_cda_prefill_varlen_v1(
     if return_dense_kv:
         return k_rot, v_rot
     return None
+
+
+def _check_raw(Q_fp16: Tensor, K_fp16: Tensor, V_fp16: Tensor, output: Tensor,
+               group_size: int, causal: bool, fn: str) -> tuple[int, int, int, int]:
+    """Shape checks of the raw-K/V prefill functions (fa2_cda.py:395-420)."""
+    if Q_fp16.dim() != 3:
+        raise ValueError("Q_fp16 must be (T, H_q, D)")
+    if K_fp16.dim() != 3 or V_fp16.dim() != 3:
+        raise ValueError("K_fp16 and V_fp16 must be (T, H_kv, D)")
+    if K_fp16.shape != V_fp16.shape:
+        raise ValueError("K_fp16 and V_fp16 shapes must match")
+    if output.shape != Q_fp16.shape:
+        raise ValueError("output shape must match Q_fp16")
+    if output.dtype != torch.float16:
+        raise ValueError("output must be fp16")
+    if not causal:
+        raise NotImplementedError(f"{fn} is causal-only")
+    T, H_q, D = Q_fp16.shape
+    if K_fp16.shape[0] != T:
+        raise ValueError("raw K/V must have the same token count as Q")
+    if K_fp16.shape[2] != D:
+        raise ValueError("Q/K/V head dimensions must match")
+    H_kv = K_fp16.shape[1]
+    if H_q != H_kv * int(group_size):
+        raise ValueError("H_q must equal H_kv * group_size")
+    return T, H_q, H_kv, D
+
+
+def _fp16c(x: Tensor) -> Tensor:
+    return (x if x.dtype == torch.float16 else x.to(torch.float16)).contiguous()
+
+
+def fa2_raw_prefill_varlen_v1(
+    Q_fp16: Tensor,           # (T, H_q, D) fp16, unrotated
+    K_fp16: Tensor,           # (T, H_kv, D) fp16, fresh uncompressed K
+    V_fp16: Tensor,           # (T, H_kv, D) fp16, fresh uncompressed V
+    cu_seqlens_q: Tensor,     # (B+1,) int32
+    output: Tensor,           # (T, H_q, D) fp16, written in place
+    *,
+    group_size: int,
+    max_query_len: int,
+    scale: Optional[float] = None,
+    causal: bool = True,
+) -> None:
+    """No-past causal prefill over the raw Q/K/V, no rotation
+    (fa2_cda.py:373-460: the reference calls vLLM's FlashAttention varlen
+    forward with cu_seqlens_k = cu_seqlens_q).  The Hadamard rotation is
+    orthonormal, so this equals attention in the rotated frame."""
+    T, H_q, H_kv, D = _check_raw(Q_fp16, K_fp16, V_fp16, output, group_size, causal,
+                                 "fa2_raw_prefill_varlen_v1")
+    if scale is None:
+        scale = 1.0 / math.sqrt(D)
+    B = int(cu_seqlens_q.numel()) - 1
+    if B <= 0 or T == 0:
+        return
+    cu = (cu_seqlens_q if cu_seqlens_q.dtype == torch.int32
+          else cu_seqlens_q.to(torch.int32)).contiguous()
+    used = (cu[1:] - cu[:-1]).contiguous()
+    out = output if output.is_contiguous() else torch.empty_like(output)
+    torch.ops.cda_hip.varlen_fwd(_fp16c(Q_fp16), _fp16c(K_fp16), _fp16c(V_fp16), out, cu, cu,
+                                 used, int(max_query_len), float(scale), True)
+    if out is not output:
+        output.copy_(out)
+
+
+def fa2_cda_prefill_rawkv_varlen_v1(
+    Q_fp16: Tensor,           # (T, H_q, D) fp16, unrotated
+    K_fp16: Tensor,           # (T, H_kv, D) fp16, fresh uncompressed K
+    V_fp16: Tensor,           # (T, H_kv, D) fp16, fresh uncompressed V
+    cu_seqlens_q: Tensor,     # (B+1,) int32
+    seq_lens: Tensor,         # (B,) int32, key lengths (= query lengths: no past)
+    output: Tensor,           # (T, H_q, D) fp16, written in place
+    *,
+    rotation_fp32: Tensor,
+    group_size: int,
+    max_query_len: int,
+    max_seq_len: int,
+    scale: Optional[float] = None,
+    causal: bool = True,
+) -> None:
+    """No-past prefill through the fused FA2-CDA kernel fed from the raw K/V
+    (fa2_cda.py:290-370): K and V rotated to fp16(x H / sqrt(128)) by the
+    Hadamard kernel (fa2_cda.py:256-287), then the fused kernel with the Q
+    Hadamard prologue and the inverse rotation of O.  The rotated rows stay
+    in their packed varlen order (cu_seqlens_k = cu_seqlens_q) instead of the
+    reference's B x max_seq_len padding; chunks with a compressed prefix
+    belong to :func:`hybrid_attn_v1`."""
+    T, H_q, H_kv, D = _check_raw(Q_fp16, K_fp16, V_fp16, output, group_size, causal,
+                                 "fa2_cda_prefill_rawkv_varlen_v1")
+    if scale is None:
+        scale = 1.0 / math.sqrt(D)
+    B = int(cu_seqlens_q.numel()) - 1
+    if B <= 0 or T == 0:
+        return
+    if int(max_query_len) > int(max_seq_len):
+        raise ValueError("raw K/V request length exceeds max_seq_len")
+    k_rot = _hadamard_or_matmul(_fp16c(K_fp16), rotation_fp32)
+    v_rot = _hadamard_or_matmul(_fp16c(V_fp16), rotation_fp32)
+    cu = (cu_seqlens_q if cu_seqlens_q.dtype == torch.int32
+          else cu_seqlens_q.to(torch.int32)).contiguous()
+    sl = (seq_lens if seq_lens.dtype == torch.int32 else seq_lens.to(torch.int32)).contiguous()
+    out = output if output.is_contiguous() else torch.empty_like(output)
+    load_fa2_cda_varlen_fused().cda_fa2_varlen_fwd_hadamard(
+        _fp16c(Q_fp16), k_rot, v_rot, out, cu, cu, sl, int(max_query_len), int(max_seq_len),
+        float(scale))
+    if out is not output:
+        output.copy_(out)
+
+
+__all__ = [
+    "fa2_cda_prefill_rawkv_varlen_v1",
+    "fa2_cda_prefill_varlen_v1",
+    "fa2_raw_prefill_varlen_v1",
+    "paged_cache_to_dense_rotated",
+]

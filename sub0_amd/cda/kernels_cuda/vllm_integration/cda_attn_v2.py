@@ -281,6 +281,7 @@ def _copy_out(output: torch.Tensor, out: torch.Tensor, T: int) -> None:
 
 _PREFILL_FUSED = ("fa2_cda_fused", "fa2_cda_auto", "fa2_cda_direct", "fa2_cda_direct_v2")
 _PREFILL_UNFUSED = ("fa2_cda",)
+_PREFILL_RAWKV = ("fa2_rawkv", "fa2_cda_rawkv", "fa2_cda_fused_rawkv")
 
 
 # ---------------------------------------------------------------------------
@@ -589,20 +590,26 @@ def _build_backend_classes():
             """Causal prefill of every query row over its request's keys
             (``cda_attn_v2.py:838-882, 1330-1472``).  ``CDA_PREFILL_BACKEND``
             picks the route: ``fa2_cda_fused`` (default), ``fa2_cda_auto``,
-            ``fa2_cda_direct[_v2]`` and ``fa2_cda`` all run the compressed-tile
-            kernel here; the raw-K/V and P34 routes are not built."""
+            ``fa2_cda_direct[_v2]`` and ``fa2_cda`` run the prefill kernel over
+            the compressed cache; ``fa2_rawkv``, ``fa2_cda_rawkv`` and
+            ``fa2_cda_fused_rawkv`` attend to the fresh fp16 K/V of the chunk
+            instead (``:1402-1441``): with a compressed prefix
+            (``max_seq_len > max_query_len``) through the hybrid kernel,
+            without one through plain FA2 (``fa2_rawkv``) or the fused FA2-CDA
+            kernel fed from the rotated raw K/V.  The P34 ``hmma`` route is not
+            built."""
             md = attn_metadata
             L = int(md.max_query_len)
             route = os.getenv("CDA_PREFILL_BACKEND", "fa2_cda_fused").lower()
-            if route not in _PREFILL_FUSED + _PREFILL_UNFUSED:
+            if route not in _PREFILL_FUSED + _PREFILL_UNFUSED + _PREFILL_RAWKV:
                 raise NotImplementedError(
                     f"CDA_PREFILL_BACKEND={route!r} is not available in the MI355X build; "
-                    f"expected one of {_PREFILL_FUSED + _PREFILL_UNFUSED}.")
+                    f"expected one of {_PREFILL_FUSED + _PREFILL_UNFUSED + _PREFILL_RAWKV}.")
             if L <= 0:
                 raise NotImplementedError("CDA prefill received an empty prefill chunk.")
             T = int(md.num_actual_tokens)
             H_q, D = self.num_heads, self.head_size
-            cb_K, cb_V, r32, _r16, flat, bs = _time_call(
+            cb_K, cb_V, r32, r16, flat, bs = _time_call(
                 "prefill_setup", lambda: self._setup(query, kv_cache))
             q = query[:T]
             if q.dtype != torch.float16:
@@ -611,13 +618,38 @@ def _build_backend_classes():
             direct = out is not None
             if not direct:
                 out = torch.empty(T, H_q, D, dtype=torch.float16, device=query.device)
-            from sub0_amd.cda.kernels_cuda.fa2_cda import fa2_cda_prefill_varlen_v1
-            _time_call("prefill_fa2_cda", lambda: fa2_cda_prefill_varlen_v1(
-                q, flat, md.block_table, md.query_start_loc, md.seq_lens, out,
-                cb_K=cb_K, cb_V=cb_V, rotation_fp32=r32, group_size=self.group_size,
-                block_size=bs, max_query_len=L, max_seq_len=md.max_seq_len,
-                scale=self.scale, causal=True,
-                fuse_fa2_epilogue=route in _PREFILL_FUSED))
+            if route in _PREFILL_RAWKV:
+                if key is None or value is None:
+                    raise ValueError(f"{route} requires fresh prefill key/value tensors")
+                k_new, v_new = key[:T], value[:T]
+                if int(md.max_seq_len) > L:
+                    from sub0_amd.cda.kernels_cuda.wrappers import hybrid_attn_v1
+                    _time_call("prefill_hybrid_rawkv_chunked", lambda: hybrid_attn_v1(
+                        q, k_new, v_new, out, flat, md.block_table,
+                        cu_seqlens_q=md.query_start_loc, seq_lens=md.seq_lens,
+                        cb_K=cb_K, cb_V=cb_V, rotation_fp32=r32, rotation_fp16=r16,
+                        scale=self.scale, group_size=self.group_size, block_size=bs,
+                        max_seq_len=int(md.max_seq_len), max_query_len=L))
+                elif route == "fa2_rawkv":
+                    from sub0_amd.cda.kernels_cuda.fa2_cda import fa2_raw_prefill_varlen_v1
+                    _time_call("prefill_fa2_rawkv", lambda: fa2_raw_prefill_varlen_v1(
+                        q, k_new, v_new, md.query_start_loc, out, group_size=self.group_size,
+                        max_query_len=L, scale=self.scale, causal=True))
+                else:
+                    from sub0_amd.cda.kernels_cuda.fa2_cda import (
+                        fa2_cda_prefill_rawkv_varlen_v1)
+                    _time_call("prefill_fa2_cda_rawkv", lambda: fa2_cda_prefill_rawkv_varlen_v1(
+                        q, k_new, v_new, md.query_start_loc, md.seq_lens, out,
+                        rotation_fp32=r32, group_size=self.group_size, max_query_len=L,
+                        max_seq_len=int(md.max_seq_len), scale=self.scale, causal=True))
+            else:
+                from sub0_amd.cda.kernels_cuda.fa2_cda import fa2_cda_prefill_varlen_v1
+                _time_call("prefill_fa2_cda", lambda: fa2_cda_prefill_varlen_v1(
+                    q, flat, md.block_table, md.query_start_loc, md.seq_lens, out,
+                    cb_K=cb_K, cb_V=cb_V, rotation_fp32=r32, group_size=self.group_size,
+                    block_size=bs, max_query_len=L, max_seq_len=md.max_seq_len,
+                    scale=self.scale, causal=True,
+                    fuse_fa2_epilogue=route in _PREFILL_FUSED))
             if not direct:
                 _time_call("prefill_output_copy", lambda: _copy_out(output, out, T))
             return output

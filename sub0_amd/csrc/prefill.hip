@@ -173,9 +173,15 @@ struct PrefillParams {
     int rotate;                 // 1: q and out unrotated (Hadamard prologue/epilogue);
                                 // 0: q and out already in the rotated frame
     int causal;                 // 1: bottom-right causal mask; 0: every key visible
-    float *part_o;              // (n_ksplit, T, H_q, 128) fp32
-    float *part_ml;             // (n_ksplit, T, H_q, 2): m (log2 domain), l
+    // Keys of sequence b: kKeysAll = [0, seq_k[b]); kKeysPast = the first
+    // seq_k[b] - (its query count) of them (the prefix before the queries);
+    // kKeysChunk = as many keys as queries (the query chunk's own keys).
+    int key_range;
+    int ks_base;                // partial slot of split 0 (several sources merged)
+    float *part_o;              // (slots, T, H_q, 128) fp32
+    float *part_ml;             // (slots, T, H_q, 2): m (log2 domain), l
 };
+constexpr int kKeysAll = 0, kKeysPast = 1, kKeysChunk = 2;
 
 // Registers holding one tile's share of the source data for this thread:
 // paged: K codes k[0..1] + nk, V codes v[0..3] (two bytes per key) + nv[];
@@ -375,7 +381,9 @@ prefill_kernel(PrefillParams p) {
 
     const int q_begin = p.cu_q[b];
     const int seq_q = p.cu_q[b + 1] - q_begin;
-    const int seq_k = p.seq_k[b];
+    const int seq_k = p.key_range == kKeysPast    ? max(0, p.seq_k[b] - seq_q)
+                      : p.key_range == kKeysChunk ? seq_q
+                                                  : p.seq_k[b];
     // Longest workgroups first: blockIdx.x counts query blocks from the end.
     // Consecutive workgroups share one (sequence, KV head) and so read the
     // same keys: ordering the grid by causal work across sequences instead
@@ -586,7 +594,7 @@ prefill_kernel(PrefillParams p) {
         // dim 32T + 8(i >> 2) + 4u + (i & 3)), columns queries.  A split that
         // saw no visible key writes O = 0, m = -inf, l = 0.
         if (qw0 + c32 < seq_q && q_begin + qw0 + c32 < p.T_total) {
-            const int64_t row = ((int64_t)ks * p.T_total + q_begin + qw0 + c32) * p.H_q + hq;
+            const int64_t row = ((int64_t)(p.ks_base + ks) * p.T_total + q_begin + qw0 + c32) * p.H_q + hq;
             float *po = p.part_o + row * kD;
 #pragma unroll
             for (int T = 0; T < 4; ++T)
@@ -764,8 +772,8 @@ prefill_combine_kernel(const float *__restrict__ part_o, const float *__restrict
                        const int32_t *__restrict__ cu_q, int B) {
     __shared__ float obs[4][kD];
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int hq = blockIdx.x * 4 + wave;
-    const int t = blockIdx.y;
+    const int hq = blockIdx.y * 4 + wave;
+    const int t = blockIdx.x;
     // Rows past the last sequence (a padded q) have no partials: leave them.
     if (t >= cu_q[B]) return;
     const int64_t split_rows = (int64_t)T * H_q;
@@ -822,12 +830,15 @@ prefill_combine_kernel(const float *__restrict__ part_o, const float *__restrict
     *reinterpret_cast<half2_ *>(out + row * kD + 2 * lane) = hv;
 }
 
+// The attention kernel alone; with `partials` it writes split partials
+// (n_ksplit of them from slot ks_base on) for prefill_combine_kernel.
 template <bool PAGED>
-int launch_prefill(const PrefillParams &p, int B, int max_q, hipStream_t st, const char *fn) {
+int launch_prefill_kernel(const PrefillParams &p, int B, int max_q, bool partials, hipStream_t st,
+                          const char *fn) {
     const int qb = 32 * (kWaves / p.GS);
     const dim3 grid((unsigned)((max_q + qb - 1) / qb * p.n_ksplit), B, p.H_kv);
     if (grid.x == 0) return CDA_OK;
-    if (PAGED && p.n_ksplit > 1) {
+    if (partials) {
         if (p.GS == 4)
             prefill_kernel<PAGED, 4, true><<<grid, kThreads, 0, st>>>(p);
         else
@@ -838,13 +849,22 @@ int launch_prefill(const PrefillParams &p, int B, int max_q, hipStream_t st, con
         prefill_kernel<PAGED, 8><<<grid, kThreads, 0, st>>>(p);
     }
     CDA_LAUNCH_CHECK(std::string(fn) + ": prefill_kernel");
-    if (p.n_ksplit > 1) {
-        // grid.y = T fits: a split grid has < 256 workgroups, so T < 256 * 64.
-        prefill_combine_kernel<<<dim3((unsigned)(p.H_q / 4), (unsigned)p.T_total), 256, 0, st>>>(
-            p.part_o, p.part_ml, p.out, p.T_total, p.H_q, p.n_ksplit, p.cu_q, B);
-        CDA_LAUNCH_CHECK(std::string(fn) + ": prefill_combine_kernel");
-    }
     return CDA_OK;
+}
+
+int launch_combine(const PrefillParams &p, int slots, int B, hipStream_t st, const char *fn) {
+    prefill_combine_kernel<<<dim3((unsigned)p.T_total, (unsigned)(p.H_q / 4)), 256, 0, st>>>(
+        p.part_o, p.part_ml, p.out, p.T_total, p.H_q, slots, p.cu_q, B);
+    CDA_LAUNCH_CHECK(std::string(fn) + ": prefill_combine_kernel");
+    return CDA_OK;
+}
+
+template <bool PAGED>
+int launch_prefill(const PrefillParams &p, int B, int max_q, hipStream_t st, const char *fn) {
+    const bool split = p.n_ksplit > 1;
+    const int rc = launch_prefill_kernel<PAGED>(p, B, max_q, split, st, fn);
+    if (rc != CDA_OK || !split) return rc;
+    return launch_combine(p, p.n_ksplit, B, st, fn);
 }
 
 // Key-split plan: split only when the unsplit grid leaves CUs idle (fewer
@@ -855,14 +875,14 @@ int launch_prefill(const PrefillParams &p, int B, int max_q, hipStream_t st, con
 constexpr int kMaxKsplit = 64;
 static_assert(kMaxKsplit <= 64, "prefill_combine_kernel: one lane per split");
 void prefill_ksplit_plan(int B, int H_q, int H_kv, int max_q, int max_k, int *n_split,
-                         int *split_tiles) {
+                         int *split_tiles, int max_split = kMaxKsplit) {
     const int qb = 32 * (kWaves / (H_q / H_kv));
     const int64_t wgs = (int64_t)((max_q + qb - 1) / qb) * B * H_kv;
     const int tiles = (max_k + kBN - 1) / kBN;
     int ns = 1;
     if (wgs > 0 && wgs < 256) {
         ns = (int)std::min<int64_t>((256 + wgs - 1) / wgs, tiles / 4);
-        ns = std::min(ns, kMaxKsplit);
+        ns = std::min(ns, max_split);
     }
     if (ns < 2) {
         *n_split = 1;
@@ -1215,4 +1235,136 @@ extern "C" int cda_hadamard128_fp16(const void *x, void *y, int64_t rows, float 
         static_cast<const uint16_t *>(x), static_cast<uint16_t *>(y), rows, scale);
     CDA_LAUNCH_CHECK("hadamard128_kernel");
     return CDA_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Hybrid chunked prefill (cda_attn_v2.py:1023-1060, 1474-1532): the queries of
+// each sequence attend to its compressed prefix in the paged cache (keys
+// [0, seq_lens[b] - q_len), all visible) and to the fresh fp16 K/V of the
+// chunk itself (causal), merged by log-sum-exp (attention.py:239-272).
+//   1. the chunk's K and V are rotated into the cache's frame,
+//      fp16(x H / sqrt(128)) (fa2_cda.py:256-287), into the workspace;
+//   2. the paged kernel over the prefix writes partials to slots [0, nA);
+//   3. the dense kernel over the rotated chunk writes slots [nA, nA + nB);
+//   4. prefill_combine_kernel merges the nA + nB slots and unrotates.
+// Workspace: the partials, then the rotated chunk K and V.
+// ---------------------------------------------------------------------------
+namespace cda {
+namespace {
+struct HybridPlan {
+    int na, na_tiles, nb, nb_tiles;
+    size_t part_bytes, kv_bytes;
+};
+
+HybridPlan hybrid_plan(int B, int T, int H_q, int H_kv, int max_query_len, int max_seq_len) {
+    HybridPlan h{};
+    prefill_ksplit_plan(B, H_q, H_kv, max_query_len, std::max(1, max_seq_len - 1), &h.na,
+                        &h.na_tiles, kMaxKsplit / 2);
+    prefill_ksplit_plan(B, H_q, H_kv, max_query_len, max_query_len, &h.nb, &h.nb_tiles,
+                        kMaxKsplit / 2);
+    h.part_bytes = prefill_ws_bytes(T, H_q, h.na + h.nb);
+    h.kv_bytes = (((size_t)T * H_kv * kD * 2) + 255) & ~(size_t)255;
+    return h;
+}
+}  // namespace
+}  // namespace cda
+
+extern "C" size_t cda_prefill_hybrid_workspace_size(int B, int T, int H_q, int H_kv,
+                                                    int max_query_len, int max_seq_len) {
+    if (B <= 0 || T <= 0 || H_q <= 0 || H_kv <= 0 || H_q % H_kv != 0 ||
+        (H_q / H_kv != 4 && H_q / H_kv != 8) || max_query_len <= 0 || max_seq_len <= 0)
+        return 0;
+    const HybridPlan h = hybrid_plan(B, T, H_q, H_kv, max_query_len, max_seq_len);
+    return h.part_bytes + 2 * h.kv_bytes;
+}
+
+extern "C" int cda_prefill_hybrid_rawkv(const void *q, const void *k_new, const void *v_new,
+                                        const void *kv_cache, int64_t num_slots, int slot_bytes,
+                                        int H_kv, const int32_t *block_table, int bt_stride,
+                                        const int32_t *cu_seqlens_q, const int32_t *seq_lens,
+                                        int B, const float *cb_k, const float *cb_v, int levels,
+                                        void *out, int T, int H_q, int block_size,
+                                        int max_query_len, int max_seq_len, float scale,
+                                        void *workspace, size_t workspace_bytes, void *stream) {
+    const char *fn = "cda_prefill_hybrid_rawkv";
+    (void)num_slots;
+    CDA_REQUIRE(q && k_new && v_new && kv_cache && block_table && cu_seqlens_q && seq_lens &&
+                    cb_k && cb_v && out,
+                "cda_prefill_hybrid_rawkv: null pointer argument");
+    CDA_REQUIRE(B >= 0 && H_kv > 0 && H_q > 0 && max_query_len >= 0 && max_seq_len >= 0,
+                "cda_prefill_hybrid_rawkv: bad B / H_q / H_kv / max_query_len / max_seq_len");
+    CDA_REQUIRE(H_q % H_kv == 0 && (H_q / H_kv == 4 || H_q / H_kv == 8),
+                "cda_prefill_hybrid_rawkv: H_q / H_kv must be 4 or 8");
+    CDA_REQUIRE(levels == 16 && slot_bytes >= 136,
+                "cda_prefill_hybrid_rawkv: the prefill reads K4V4 caches (16 levels, slot >= 136 B)");
+    CDA_REQUIRE(block_size > 0 && block_size % 16 == 0 && bt_stride > 0,
+                "cda_prefill_hybrid_rawkv: block_size must be a positive multiple of 16");
+    CDA_REQUIRE(((uintptr_t)q & 15) == 0 && ((uintptr_t)out & 15) == 0 &&
+                    ((uintptr_t)k_new & 15) == 0 && ((uintptr_t)v_new & 15) == 0 &&
+                    ((uintptr_t)kv_cache & 7) == 0 && slot_bytes % 8 == 0,
+                "cda_prefill_hybrid_rawkv: q/out/k_new/v_new must be 16-byte and the cache "
+                "8-byte aligned");
+    if (B == 0 || max_query_len == 0) return CDA_OK;
+    CDA_REQUIRE(T > 0, "cda_prefill_hybrid_rawkv: T must be the number of query rows");
+    const HybridPlan h = hybrid_plan(B, T, H_q, H_kv, max_query_len, std::max(1, max_seq_len));
+    const size_t need = h.part_bytes + 2 * h.kv_bytes;
+    if (!workspace || workspace_bytes < need || ((uintptr_t)workspace & 255))
+        return fail(CDA_E_WORKSPACE, "cda_prefill_hybrid_rawkv: workspace missing, misaligned or "
+                                     "smaller than cda_prefill_hybrid_workspace_size()");
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    char *ws = static_cast<char *>(workspace);
+    uint16_t *k_rot = reinterpret_cast<uint16_t *>(ws + h.part_bytes);
+    uint16_t *v_rot = reinterpret_cast<uint16_t *>(ws + h.part_bytes + h.kv_bytes);
+    const int64_t kv_rows = (int64_t)T * H_kv;
+    const float hs = 0.08838834764831845f;
+    hadamard128_kernel<<<(unsigned)((kv_rows + 15) / 16), 256, 0, st>>>(
+        static_cast<const uint16_t *>(k_new), k_rot, kv_rows, hs);
+    CDA_LAUNCH_CHECK("cda_prefill_hybrid_rawkv: hadamard128_kernel (K)");
+    hadamard128_kernel<<<(unsigned)((kv_rows + 15) / 16), 256, 0, st>>>(
+        static_cast<const uint16_t *>(v_new), v_rot, kv_rows, hs);
+    CDA_LAUNCH_CHECK("cda_prefill_hybrid_rawkv: hadamard128_kernel (V)");
+
+    PrefillParams p{};
+    p.q = static_cast<const uint16_t *>(q);
+    p.out = static_cast<uint16_t *>(out);
+    p.cu_q = cu_seqlens_q;
+    p.seq_k = seq_lens;
+    p.H_q = H_q;
+    p.H_kv = H_kv;
+    p.GS = H_q / H_kv;
+    p.scale_log2 = scale * kLog2e;
+    p.kv = static_cast<const uint8_t *>(kv_cache);
+    p.block_table = block_table;
+    p.bt_stride = bt_stride;
+    p.block_size = block_size;
+    p.bs_shift = (block_size & (block_size - 1)) == 0 ? __builtin_ctz(block_size) : -1;
+    p.slot_bytes = slot_bytes;
+    p.row_bytes = (int64_t)H_kv * slot_bytes;
+    p.cb_k = cb_k;
+    p.cb_v = cb_v;
+    p.T_total = T;
+    p.rotate = 1;
+    p.part_o = reinterpret_cast<float *>(ws);
+    p.part_ml = reinterpret_cast<float *>(
+        ws + (((size_t)(h.na + h.nb) * T * H_q * cda::kD * 4 + 255) & ~(size_t)255));
+    // The compressed prefix: every key precedes every query of the chunk.
+    p.causal = 0;
+    p.key_range = kKeysPast;
+    p.ks_base = 0;
+    p.n_ksplit = h.na;
+    p.ksplit_tiles = h.na_tiles;
+    int rc = launch_prefill_kernel<true>(p, B, max_query_len, true, st, fn);
+    if (rc != CDA_OK) return rc;
+    // The chunk's own keys, causal; dense rows of sequence b start at cu_q[b].
+    p.causal = 1;
+    p.key_range = kKeysChunk;
+    p.ks_base = h.na;
+    p.n_ksplit = h.nb;
+    p.ksplit_tiles = h.nb_tiles;
+    p.k_rot = k_rot;
+    p.v_rot = v_rot;
+    p.cu_k = cu_seqlens_q;
+    rc = launch_prefill_kernel<false>(p, B, max_query_len, true, st, fn);
+    if (rc != CDA_OK) return rc;
+    return launch_combine(p, h.na + h.nb, B, st, fn);
 }

@@ -125,9 +125,12 @@ def test_prefill_route_errors(monkeypatch):
     q = torch.zeros(4, 32, 128, dtype=torch.float16)
     cache = A._as_uint8_cache(torch.zeros(2, 16, 8, 72, dtype=torch.float16))
     md = _meta(max_query_len=2, num_actual_tokens=4)
-    monkeypatch.setenv("CDA_PREFILL_BACKEND", "fa2_rawkv")
+    monkeypatch.setenv("CDA_PREFILL_BACKEND", "hmma")
     with pytest.raises(NotImplementedError):
         impl._forward_prefill(q, q, q, q, md, cache)
+    monkeypatch.setenv("CDA_PREFILL_BACKEND", "fa2_rawkv")
+    with pytest.raises(ValueError, match="fresh prefill key/value"):
+        impl._forward_prefill(q, None, None, q, md, cache)
     monkeypatch.setenv("CDA_PREFILL_BACKEND", "fa2_cda_fused")
     with pytest.raises(NotImplementedError):
         impl._forward_prefill(q, q, q, q, _meta(max_query_len=0), cache)

@@ -58,6 +58,7 @@ class Scenario:
         self.lens += np.asarray(new, dtype=np.int32)
         K = np.concatenate(rows_k)
         V = np.concatenate(rows_v)
+        self.last_kv = (K, V)
         Q = np.concatenate(rows_q)
         sm = np.concatenate(slots)
         T = len(sm)
@@ -167,3 +168,25 @@ def test_backend_long_prefill_takes_dense_bridge(gpu, monkeypatch):
     print("[backend] decode after the long prefill", flush=True)
     out, cache, Q, cu = sc.step([1, 1, 1])
     check(out, sc.expected_decode(cache, Q, cu, [0, 1, 2]))
+
+
+@pytest.mark.parametrize("route", ["fa2_rawkv", "fa2_cda_rawkv", "fa2_cda_fused_rawkv"])
+def test_backend_rawkv_routes(gpu, monkeypatch, route):
+    """CDA_PREFILL_BACKEND raw-K/V routes (cda_attn_v2.py:1402-1441): a first
+    prefill (no prefix: FA2 over the fresh K/V, unrotated for fa2_rawkv,
+    rotated otherwise) then a chunked-prefill step
+    (compressed prefix + fresh chunk: the hybrid kernel), each against the
+    checker's hybrid_prefill on the cache the GPU wrote."""
+    monkeypatch.setenv("CDA_PREFILL_BACKEND", route)
+    sc = Scenario(gpu, seed=80)
+    for lens in ([37, 100, 64], [20, 5, 33]):
+        print(f"[backend] {route} step {lens}", flush=True)
+        out, cache, Q, cu = sc.step(lens)
+        K, V = sc.last_kv
+        if route == "fa2_rawkv" and int(sc.lens.max()) == max(lens):
+            from tests.cases import raw_causal_attention
+            exp = raw_causal_attention(Q, np.asarray(cu, np.int32), K, V)
+        else:
+            exp = O.hybrid_prefill(Q, np.asarray(cu, np.int32), K, V, cache, sc.bt, sc.lens,
+                                   sc.cb, sc.cb, O.hadamard128(), H_kv=H_KV, block_size=BS)
+        check(out, exp)

@@ -252,3 +252,56 @@ def test_causal_prefill_last_row_is_decode():
         d = O.decode_paged(q[i:i + 1], c["cache"], c["bt"], sl, c["cb"], c["cb"], R,
                            H_kv=c["H_kv"], block_size=c["bs"])
         assert np.array_equal(pre[i], d[0])
+
+
+def test_paged_rows_are_the_encoded_rows():
+    """paged_rows reads sequence b's keys through the permuted block table:
+    equal to decoding the encodings the cache was built from."""
+    from tests.cases import make_hybrid_case
+    c = make_hybrid_case(71, [3, 5], [37, 20], H_kv=2)
+    kp, kn = c.k_enc
+    for b, n in enumerate(c.seq_k):
+        k, _ = O.paged_rows(c.cache, c.block_table, b, int(n), c.cb, c.cb, H_kv=2,
+                            block_size=c.block_size)
+        assert np.array_equal(k.view(np.uint16),
+                              O.decode_rotated(kp[b, :, :n], kn[b, :, :n], c.cb).view(np.uint16))
+
+
+def test_hybrid_merge_equals_one_softmax():
+    """hybrid_prefill (two partials + merge_partials) equals one float64
+    softmax over [decoded prefix; rotated raw chunk] with the prefix visible to
+    every query and the chunk causal; and the no-prefix case reduces to plain
+    causal attention over the raw chunk in the unrotated frame (R orthonormal:
+    within fp16 rounding)."""
+    from tests.cases import make_hybrid_case
+    c = make_hybrid_case(72, [4, 6, 3], [30, 6, 19], H_kv=2, gs=4)
+    R = O.hadamard128().astype(np.float64)
+    s = 1.0 / np.sqrt(128)
+    q_rot = (c.q.astype(np.float32) @ R.astype(np.float32)).astype(np.float16)
+    k_rot = (c.k_new.astype(np.float32) @ R.astype(np.float32)).astype(np.float16)
+    v_rot = (c.v_new.astype(np.float32) @ R.astype(np.float32)).astype(np.float16)
+    for b in range(3):
+        q0, q1 = c.cu_q[b], c.cu_q[b + 1]
+        n = q1 - q0
+        past = c.seq_k[b] - n
+        kp, vp = O.paged_rows(c.cache, c.block_table, b, past, c.cb, c.cb, H_kv=2,
+                              block_size=c.block_size)
+        for hq in range(8):
+            h = hq // 4
+            K = np.concatenate([kp[h], k_rot[q0:q1, h]]).astype(np.float64)
+            V = np.concatenate([vp[h], v_rot[q0:q1, h]]).astype(np.float64)
+            sc = q_rot[q0:q1, hq].astype(np.float64) @ K.T * s
+            vis = np.arange(past + n)[None, :] <= past + np.arange(n)[:, None]
+            sc = np.where(vis, sc, -np.inf)
+            p = np.exp(sc - sc.max(1, keepdims=True))
+            o = ((p @ V) / p.sum(1, keepdims=True)).astype(np.float16)
+            exp = (o.astype(np.float32) @ R.T.astype(np.float32)).astype(np.float16)
+            got = c.expected[q0:q1, hq]
+            assert np.abs(got.astype(np.float32) - exp.astype(np.float32)).max() <= 1e-3
+            if past == 0:
+                kk = c.k_new[q0:q1, h].astype(np.float64)
+                vv = c.v_new[q0:q1, h].astype(np.float64)
+                sc2 = np.where(vis, c.q[q0:q1, hq].astype(np.float64) @ kk.T * s, -np.inf)
+                p2 = np.exp(sc2 - sc2.max(1, keepdims=True))
+                o2 = (p2 @ vv) / p2.sum(1, keepdims=True)
+                assert np.abs(got.astype(np.float64) - o2).max() <= 4e-3
