@@ -50,7 +50,7 @@ def log(*a):
 # --------------------------------------------------------------- workload --
 
 def make_workload(B: int, N: int, dev, seed: int | None = None, identity_bt: bool = False,
-                  levels: int = 16):
+                  levels: int = 16, k_uniform: bool = False):
     """Paged K4V4 (levels 16, 144-byte slots) or K2V2 (levels 4, 80-byte
     slots) cache of B sequences x N tokens, encoded on the GPU by the fused
     encoder from K, V ~ N(0,1) fp16 (K with 4 seeded outlier channels x8),
@@ -69,6 +69,9 @@ def make_workload(B: int, N: int, dev, seed: int | None = None, identity_bt: boo
     cache = torch.zeros(B * nb * BS, H_KV, 144 if levels == 16 else 80, dtype=torch.uint8,
                         device=dev)
     cb = lloyd_max_centroids_beta(levels, D).to(dev)
+    # k_uniform: K codes from the uniform codebook (the score-domain QK option)
+    from sub0_amd.cda.algorithm.compression import uniform_centroids
+    cbk = uniform_centroids(levels).to(dev) if k_uniform else cb
     chunk = 1 << 16                                    # tokens per encode launch
     pos = torch.arange(N, device=dev, dtype=torch.int64)
     for b in range(B):
@@ -78,13 +81,13 @@ def make_workload(B: int, N: int, dev, seed: int | None = None, identity_bt: boo
             k = torch.randn(t1 - t0, H_KV, D, generator=gpu, device=dev, dtype=torch.float16)
             k[..., outl] *= 8
             v = torch.randn(t1 - t0, H_KV, D, generator=gpu, device=dev, dtype=torch.float16)
-            _native.paged_encode(k, v, slots_b[t0:t1].contiguous(), cache, cb, cb)
+            _native.paged_encode(k, v, slots_b[t0:t1].contiguous(), cache, cbk, cb)
     q = torch.randn(B, H_Q, D, generator=gpu, device=dev, dtype=torch.float16)
     seq = torch.full((B,), N, dtype=torch.int32, device=dev)
     R = hadamard_matrix(D).to(dev)
     torch.cuda.synchronize()
-    return dict(q=q, cache=cache, bt=bt, seq=seq, cb=cb, R=R, R16=R.half(),
-                out=torch.empty_like(q), B=B, N=N)
+    return dict(q=q, cache=cache, bt=bt, seq=seq, cb=cb, cbk=cbk, R=R, R16=R.half(),
+                out=torch.empty_like(q), B=B, N=N, uniform_qk=k_uniform)
 
 
 def make_prefill_workload(dev, seed: int = 0xCDA3, n_seq: int = 8, lo: int = 512,
@@ -793,9 +796,10 @@ def decode_call(w, tile_n: int = 0):
         return call
 
     def call():
-        decode_hmma_v1(w["q"], w["cache"], w["bt"], w["seq"], w["out"], cb_K=w["cb"],
+        decode_hmma_v1(w["q"], w["cache"], w["bt"], w["seq"], w["out"], cb_K=w["cbk"],
                        cb_V=w["cb"], rotation_fp32=w["R"], rotation_fp16=w["R16"],
-                       group_size=H_Q // H_KV, block_size=BS, max_seq_len=w["N"])
+                       group_size=H_Q // H_KV, block_size=BS, max_seq_len=w["N"],
+                       qk_without_k_decode=w["uniform_qk"])
     return call
 
 
@@ -1018,6 +1022,9 @@ def main(argv=None):
                          "comparators and fp16 attention")
     ap.add_argument("--gs8", action="store_true",
                     help="GQA group of 8 (64 Q / 8 KV heads, the 70B shape) instead of 4")
+    ap.add_argument("--uniform-qk", action="store_true",
+                    help="decode a cache with the uniform 16-level K codebook through the "
+                         "score-domain QK option (attention.py:101-187)")
     ap.add_argument("--k2v2", action="store_true",
                     help="decode over a K2V2 cache (4-level codebook, 80-byte slots) instead of K4V4")
     ap.add_argument("--general-kernel", action="store_true",
@@ -1065,7 +1072,8 @@ def main(argv=None):
     if args.gs8:
         H_Q = 8 * H_KV
     levels = 4 if args.k2v2 else 16
-    w = make_workload(B, N, dev, identity_bt=args.identity_block_table, levels=levels)
+    w = make_workload(B, N, dev, identity_bt=args.identity_block_table, levels=levels,
+                      k_uniform=args.uniform_qk)
     fn = decode_call(w, args.tile_n)
     g = capture(fn, args.warmup)
     settle(g)
@@ -1116,7 +1124,7 @@ def main(argv=None):
 
     cpu = None
     # the CPU baseline is config 0 (K4V4, 32 Q heads)
-    if not args.no_cpu_baseline and levels == 16 and not args.gs8:
+    if not args.no_cpu_baseline and levels == 16 and not args.gs8 and not args.uniform_qk:
         try:
             cpu = cpu_baseline()
         except Exception as e:  # the baseline is reported, never required
@@ -1127,8 +1135,12 @@ def main(argv=None):
     # Both code widths (8 KV heads, one codebook) take the page-streaming kernel
     # unless it is switched off.
     kernel = "decode_split_kernel" if args.general_kernel else "decode_stream_kernel"
-    traffic = load_traffic(kernel, B, N) if levels == 16 and not args.gs8 else None
+    traffic = (load_traffic(kernel, B, N) if levels == 16 and not args.gs8
+               and not args.uniform_qk else None)
     variant = "K4V4" if levels == 16 else "K2V2"
+    if args.uniform_qk:
+        variant += " (uniform K codebook, score-domain QK)"
+        kernel = "decode_stream_kernel<SQK>"
     line = {
         "metric": METRIC,
         "value": round(value, 1),

@@ -88,6 +88,38 @@ int cda_decode_full_hmma_v3_k4v2(const void *q, const void *kv_cache, int64_t nu
                                  int tile_n, int max_seq_len, float scale, void *workspace,
                                  size_t workspace_bytes, void *stream);
 
+/* Decode with the score-domain QK of the reference's
+ * qk_scores_uniform_4bit_without_k_decode / attention_compressed_rotated_
+ * reference_qk_without_k_decode (cda/algorithm/attention.py:101-187) for a
+ * K4V4 cache whose K codebook is the 16-level uniform one, cb[i] = (2i+1)/16 - 1
+ * (compression.py:75-83): score = Kn * (q_rot . code / 8 - 15/16 sum(q_rot))
+ * * scale from the integer codes (K never decoded), V decoded as fp16(cb_v *
+ * Vn).  The reference has no kernel for it (its torch function is the
+ * contract).  Same arguments as cda_decode_full_hmma_v3 (levels 16 implied,
+ * no fp16 rotation); needs H_kv = 8, 144-byte slots and splits of at most
+ * 16384 tokens (CDA_E_INVALID otherwise).  cb_k is checked on the device: if
+ * it is not the uniform codebook the output is NaN. */
+int cda_decode_full_hmma_v3_uniform_qk(const void *q, const void *kv_cache, int64_t num_slots,
+                                       int slot_bytes, int H_kv, const int32_t *block_table,
+                                       int bt_stride, const int32_t *seq_lens, const float *cb_k,
+                                       const float *cb_v, const float *rot_f32, void *out, int B,
+                                       int H_q, int group_size, int block_size, int tile_n,
+                                       int max_seq_len, float scale, void *workspace,
+                                       size_t workspace_bytes, void *stream);
+
+/* Score-domain QK scores over contiguous compressed K
+ * (qk_scores_uniform_4bit_without_k_decode, cda/algorithm/attention.py:101-152):
+ *   q_rot:  (B, H_q, M_q, 128) fp16, rotated frame
+ *   k_idx:  (B, H_kv, M_k, 64) uint8, 4-bit codes MSB-first, 16-byte aligned
+ *   k_norm: (B, H_kv, M_k) fp32
+ *   out:    (B, H_q, M_q, key_end - key_start) fp32 =
+ *           k_norm * (q_rot . code / 8 - 15/16 sum(q_rot)) * scale, -inf where
+ *           causal and key_start + k > m + q_offset. */
+int cda_qk_scores_uniform4(const void *q_rot, const void *k_idx, const float *k_norm,
+                           float *out, int B, int H_q, int H_kv, int M_q, int group_size,
+                           int64_t M_k, int64_t key_start, int64_t key_end, int64_t q_offset,
+                           float scale, int causal, void *stream);
+
 /* Allocation-free variant of cda_decode_full_hmma_v3.  No counterpart in the
  * reference: it is for callers that cannot allocate device memory (code
  * under graph capture that must not call hipMalloc, tight serving loops,

@@ -11,6 +11,9 @@ pure-torch oracle, so that on the CPU it gives the reference's bits:
 * ``pack4`` / ``unpack4``        cda/algorithm/compression.py:163-188
 * ``gqa_attention``              cda/algorithm/attention.py:60-93
 * ``attention_compressed``       cda/algorithm/attention.py:306-346, 426-482
+* ``causal_mask``                cda/algorithm/attention.py:46-57
+* ``qk_scores_uniform4``         cda/algorithm/attention.py:101-152
+* ``attention_qk_uniform4``      cda/algorithm/attention.py:155-187
 
 ``bench.py`` times it as the CPU baseline ("the reference's CPU algorithm
 path"), and tests/ pin it against the reference-written golden fixtures.
@@ -97,3 +100,54 @@ def attention_compressed(q: torch.Tensor, k_codes, k_norm, v_codes, v_norm,
     v = decode_rows(v_codes, v_norm, cb)
     o_rot = gqa_attention(q_rot, k, v, group_size)
     return unrotate(o_rot, H).to(torch.float16)
+
+
+def causal_mask(m_q: int, m_k: int, q_offset: int = 0) -> torch.Tensor:
+    """(M_q, M_k) bool, key k visible to query q iff k <= q + q_offset (:46-57)."""
+    q = torch.arange(m_q).unsqueeze(1) + q_offset
+    k = torch.arange(m_k).unsqueeze(0)
+    return k <= q
+
+
+def qk_scores_uniform4(q_rot: torch.Tensor, k_idx: torch.Tensor, k_norm: torch.Tensor,
+                       group_size: int, scale: float | None = None, causal: bool = False,
+                       q_offset: int = 0, key_start: int = 0, key_end: int | None = None):
+    """Score-domain QK for the 16-level uniform codebook (:101-152):
+    norm * ((Q @ code) / 8 - 15/16 * sum(Q)) * scale, codes never decoded.
+    q_rot (B, H_q, M_q, 128); k_idx (B, H_kv, M_k, 64) uint8; k_norm (B, H_kv,
+    M_k).  Returns (B, H_kv, g, M_q, key_end - key_start) fp32."""
+    B, H_q, M_q, D = q_rot.shape
+    H_kv = k_idx.shape[1]
+    n_keys = k_norm.shape[-1]
+    if key_end is None:
+        key_end = n_keys
+    if scale is None:
+        scale = 1.0 / math.sqrt(D)
+    kid = k_idx[..., key_start:key_end, :]
+    kn = k_norm[..., key_start:key_end].float()
+    codes = unpack4(kid).float()
+    qg = q_rot.float().view(B, H_kv, group_size, M_q, D)
+    q_code = torch.einsum("bhgmd,bhkd->bhgmk", qg, codes)
+    q_sum = qg.sum(dim=-1).unsqueeze(-1)
+    scores = kn.unsqueeze(2).unsqueeze(3) * (q_code * 0.125 - q_sum * 0.9375)
+    scores = scores * scale
+    if causal:
+        mask = causal_mask(M_q, key_end - key_start, q_offset - key_start)
+        scores = scores.masked_fill(~mask, float("-inf"))
+    return scores
+
+
+def attention_qk_uniform4(q_rot, k_idx, k_norm, v_idx, v_norm, cb_v, group_size,
+                          scale=None, causal=False, q_offset=0, key_start=0, key_end=None):
+    """Score-domain QK, softmax, decoded V (:155-187); fp16 (B, H_q, M_q, 128)
+    in the rotated frame."""
+    if key_end is None:
+        key_end = k_norm.shape[-1]
+    scores = qk_scores_uniform4(q_rot, k_idx[..., key_start:key_end, :],
+                                k_norm[..., key_start:key_end], group_size, scale, causal,
+                                q_offset - key_start if causal else q_offset)
+    v = decode_rows(v_idx[..., key_start:key_end, :], v_norm[..., key_start:key_end], cb_v)
+    p = torch.softmax(scores, dim=-1)
+    B, H_q, M_q, D = q_rot.shape
+    out = torch.einsum("bhgmk,bhkd->bhgmd", p, v.float())
+    return out.reshape(B, H_q, M_q, D).to(torch.float16)

@@ -44,6 +44,8 @@ SYMBOLS = (
     "cda_hadamard128_fp16",
     "cda_prefill_hybrid_workspace_size",
     "cda_prefill_hybrid_rawkv",
+    "cda_decode_full_hmma_v3_uniform_qk",
+    "cda_qk_scores_uniform4",
 )
 
 
@@ -124,6 +126,14 @@ def lib():
         L.cda_prefill_paged_hadamard_ws.argtypes = [
             _P, _P, _I64, _I32, _I32, _P, _I32, _P, _P, _I32, _P, _P, _I32, _P, _I32, _I32,
             _I32, _I32, _I32, _F32, _P, _SZ, _P]
+        L.cda_decode_full_hmma_v3_uniform_qk.restype = _I32
+        L.cda_decode_full_hmma_v3_uniform_qk.argtypes = [
+            _P, _P, _I64, _I32, _I32, _P, _I32, _P, _P, _P, _P, _P, _I32, _I32, _I32, _I32,
+            _I32, _I32, _F32, _P, _SZ, _P]
+        L.cda_qk_scores_uniform4.restype = _I32
+        L.cda_qk_scores_uniform4.argtypes = [
+            _P, _P, _P, _P, _I32, _I32, _I32, _I32, _I32, _I64, _I64, _I64, _I64, _F32, _I32,
+            _P]
         L.cda_prefill_hybrid_workspace_size.restype = _SZ
         L.cda_prefill_hybrid_workspace_size.argtypes = [_I32, _I32, _I32, _I32, _I32, _I32]
         L.cda_prefill_hybrid_rawkv.restype = _I32
@@ -193,12 +203,16 @@ def decode(q: torch.Tensor, kv_cache: torch.Tensor, block_table: torch.Tensor,
            seq_lens: torch.Tensor, cb_k: torch.Tensor, cb_v: torch.Tensor,
            rot_f32: torch.Tensor, rot_f16: torch.Tensor | None, out: torch.Tensor, *,
            group_size: int, block_size: int, tile_n: int, max_seq_len: int, scale: float,
-           workspace: torch.Tensor | None = None) -> None:
+           workspace: torch.Tensor | None = None, uniform_qk: bool = False) -> None:
     """Split-K decode over the paged cache; ``out`` is written in place.
 
     q (B, H_q, 128) fp16; kv_cache (num_slots, H_kv, slot_bytes) uint8;
     block_table (B, W) int32; seq_lens (B,) int32; cb_* (16,) fp32;
     rot_f32 (128, 128) fp32; out (B, H_q, 128) fp16.
+
+    ``uniform_qk``: score-domain QK (attention.py:101-152) for a cb_K equal to
+    the 16-level uniform codebook, K4V4 144-byte slots and 8 KV heads; the
+    kernel checks cb_K on the device and writes NaN if it differs.
     """
     dev = _require_gpu(q, kv_cache, block_table, seq_lens, cb_k, cb_v, rot_f32, out)
     if q.dtype != torch.float16 or out.dtype != torch.float16:
@@ -235,6 +249,16 @@ def decode(q: torch.Tensor, kv_cache: torch.Tensor, block_table: torch.Tensor,
         workspace = torch.empty(need + 256, dtype=torch.uint8, device=dev)
     ws_ptr = workspace.data_ptr()
     pad = (-ws_ptr) % 256
+    if uniform_qk:
+        if cb_k.numel() != 16 or cb_v.numel() != 16:
+            raise ValueError("the score-domain QK reads K4V4 caches (16-level codebooks)")
+        rc = lib().cda_decode_full_hmma_v3_uniform_qk(
+            _ptr(q), _ptr(kv_cache), num_slots, slot_bytes, H_kv, _ptr(block_table),
+            block_table.stride(0), _ptr(seq_lens), _ptr(cb_k), _ptr(cb_v), _ptr(rot_f32),
+            _ptr(out), B, H_q, int(group_size), int(block_size), int(tile_n), int(max_seq_len),
+            float(scale), ctypes.c_void_p(ws_ptr + pad), workspace.numel() - pad, _stream(dev))
+        _check(rc, "cda_decode_full_hmma_v3_uniform_qk")
+        return
     if k4v2:
         rc = lib().cda_decode_full_hmma_v3_k4v2(
             _ptr(q), _ptr(kv_cache), num_slots, slot_bytes, H_kv, _ptr(block_table),
@@ -251,6 +275,31 @@ def decode(q: torch.Tensor, kv_cache: torch.Tensor, block_table: torch.Tensor,
         int(block_size), int(tile_n), int(max_seq_len), float(scale),
         ctypes.c_void_p(ws_ptr + pad), workspace.numel() - pad, _stream(dev))
     _check(rc, "cda_decode_full_hmma_v3")
+
+
+def qk_scores_uniform4(q_rot: torch.Tensor, k_idx: torch.Tensor, k_norm: torch.Tensor,
+                       out: torch.Tensor, *, group_size: int, scale: float, causal: bool,
+                       q_offset: int, key_start: int, key_end: int) -> None:
+    """Score-domain QK over contiguous compressed K (``cda_qk_scores_uniform4``):
+    q_rot (B, H_q, M_q, 128) fp16, k_idx (B, H_kv, M_k, 64) uint8, k_norm
+    (B, H_kv, M_k) fp32 -> out (B, H_q, M_q, key_end - key_start) fp32."""
+    dev = _require_gpu(q_rot, k_idx, k_norm, out)
+    if q_rot.dtype != torch.float16 or k_idx.dtype != torch.uint8:
+        raise TypeError("Q_rot must be fp16 and K idx uint8")
+    if k_norm.dtype != torch.float32 or out.dtype != torch.float32:
+        raise TypeError("K norm and the scores must be fp32")
+    for t in (q_rot, k_idx, k_norm, out):
+        if not t.is_contiguous():
+            raise ValueError("Q_rot, K idx / norm and the scores must be contiguous")
+    B, H_q, M_q, _ = q_rot.shape
+    H_kv, M_k = k_idx.shape[1], k_idx.shape[2]
+    if out.shape != (B, H_q, M_q, key_end - key_start):
+        raise ValueError("scores must be (B, H_q, M_q, key_end - key_start)")
+    rc = lib().cda_qk_scores_uniform4(
+        _ptr(q_rot), _ptr(k_idx), _ptr(k_norm), _ptr(out), B, H_q, H_kv, M_q, int(group_size),
+        M_k, int(key_start), int(key_end), int(q_offset), float(scale), int(bool(causal)),
+        _stream(dev))
+    _check(rc, "cda_qk_scores_uniform4")
 
 
 def set_split_timing_events(start=None, stop=None) -> None:

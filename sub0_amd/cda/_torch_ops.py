@@ -9,8 +9,8 @@ implementations that call the C ABI of ``libcda_hip.so`` through
 ``torch.ops.cda_hip`` -- the product entry points the reference reaches
 through its pybind modules (``cda/kernels_cuda/wrappers.py:115-124,
 153-156``, ``fa2_cda.py:51-52, 85-95, 166-181``): ``decode``, ``encode``,
-``prefill``, ``prefill_hybrid``, ``paged_to_dense``, ``varlen_fwd_hadamard``,
-``varlen_fwd``, ``hadamard128``.
+``decode_uniform_qk``, ``qk_scores_uniform4``, ``prefill``, ``prefill_hybrid``,
+``paged_to_dense``, ``varlen_fwd_hadamard``, ``varlen_fwd``, ``hadamard128``.
 ``load_pybind_module`` routes its module functions through these ops.
 
 ``torch.ops._cda_vllm_fa2_fork_C`` -- the comparator namespace of the
@@ -49,6 +49,20 @@ def _decode(q, kv_cache, block_table, seq_lens, cb_k, cb_v, rot_f32, rot_f16, ou
     _native.decode(q, kv_cache, block_table, seq_lens, cb_k, cb_v, rot_f32, rot_f16, out,
                    group_size=group_size, block_size=block_size, tile_n=tile_n,
                    max_seq_len=max_seq_len, scale=scale)
+
+
+def _decode_uniform_qk(q, kv_cache, block_table, seq_lens, cb_k, cb_v, rot_f32, out,
+                       group_size, block_size, tile_n, max_seq_len, scale):
+    _native.decode(q, kv_cache, block_table, seq_lens, cb_k, cb_v, rot_f32, None, out,
+                   group_size=group_size, block_size=block_size, tile_n=tile_n,
+                   max_seq_len=max_seq_len, scale=scale, uniform_qk=True)
+
+
+def _qk_scores(q_rot, k_idx, k_norm, out, group_size, scale, causal, q_offset, key_start,
+               key_end):
+    _native.qk_scores_uniform4(q_rot, k_idx, k_norm, out, group_size=group_size, scale=scale,
+                               causal=causal, q_offset=q_offset, key_start=key_start,
+                               key_end=key_end)
 
 
 def _encode(k, v, slot_mapping, flat_cache, cb_k, cb_v):
@@ -103,6 +117,13 @@ _define(_cda, "decode(Tensor q, Tensor kv_cache, Tensor block_table, Tensor seq_
               "Tensor cb_k, Tensor cb_v, Tensor rot_f32, Tensor rot_f16, Tensor(a!) out, "
               "int group_size, int block_size, int tile_n, int max_seq_len, float scale) -> ()",
         _decode, _nothing)
+_define(_cda, "decode_uniform_qk(Tensor q, Tensor kv_cache, Tensor block_table, "
+              "Tensor seq_lens, Tensor cb_k, Tensor cb_v, Tensor rot_f32, Tensor(a!) out, "
+              "int group_size, int block_size, int tile_n, int max_seq_len, float scale) -> ()",
+        _decode_uniform_qk, _nothing)
+_define(_cda, "qk_scores_uniform4(Tensor q_rot, Tensor k_idx, Tensor k_norm, Tensor(a!) out, "
+              "int group_size, float scale, bool causal, int q_offset, int key_start, "
+              "int key_end) -> ()", _qk_scores, _nothing)
 _define(_cda, "encode(Tensor k, Tensor v, Tensor slot_mapping, Tensor(a!) flat_cache, "
               "Tensor cb_k, Tensor cb_v) -> ()", _encode, _nothing)
 _define(_cda, "prefill(Tensor q, Tensor kv_cache, Tensor block_table, Tensor cu_seqlens_q, "

@@ -70,11 +70,18 @@ def decode_hmma_v1(
     block_size: int,
     scale: Optional[float] = None,
     max_seq_len: Optional[int] = None,
+    qk_without_k_decode: bool = False,
 ) -> None:
     """Single-query split-K decode (K4V4), output written in place.
 
     Graph-capturable when ``max_seq_len`` is given (no host sync); the split-K
     workspace comes from the caching allocator on the current stream.
+
+    ``qk_without_k_decode`` (no counterpart in the reference's wrapper): the
+    score-domain QK of ``attention.py:101-187`` for caches whose K codebook
+    is the 16-level uniform one -- scores from the integer codes and the K
+    norm, V decoded as usual.  Needs 8 KV heads and 144-byte slots; a cb_K
+    other than uniform_centroids(16) gives NaN output.
     """
     B, H_q, D = Q_fp16.shape
     if scale is None:
@@ -89,6 +96,15 @@ def decode_hmma_v1(
         Q_fp16 = Q_fp16.to(torch.float16)
     if output.dtype != torch.float16:
         raise ValueError("decode_hmma_v1 requires fp16 output buffer")
+    if qk_without_k_decode:
+        torch.ops.cda_hip.decode_uniform_qk(
+            Q_fp16.contiguous(), kv_cache.view(-1, *kv_cache.shape[-2:]),
+            block_table.to(torch.int32) if block_table.dtype != torch.int32 else block_table,
+            seq_lens.to(torch.int32) if seq_lens.dtype != torch.int32 else seq_lens,
+            cb_K.float().contiguous(), cb_V.float().contiguous(),
+            rotation_fp32.float().contiguous(), output, group_size, block_size, tile_N,
+            max_seq_len, scale)
+        return
 
     mod.cda_decode_full_hmma_v3(
         Q_fp16.contiguous(),

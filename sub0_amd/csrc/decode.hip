@@ -72,6 +72,9 @@ struct SplitParams {
     // pointers): 1 if they hold equal bits.  The page-streaming kernel runs
     // only if 1, the general kernel only if 0.
     const int *cb_same;
+    // Score-domain QK (decode_stream_kernel's SQK form): 1 if cb_k holds the
+    // 16-level uniform codebook (2i + 1)/16 - 1, written by rotate_q_kernel.
+    const int *k_uniform;
 };
 
 __device__ __forceinline__ floatx4 mfma16(uint4 a, uint4 b, floatx4 c) {
@@ -541,11 +544,18 @@ __device__ __forceinline__ uint32_t bfi(uint32_t m, uint32_t a, uint32_t b) {
     return (m & a) | (~m & b);
 }
 
-template <int GS, int L>
+// SQK: score-domain QK for the 16-level uniform K codebook
+// (attention.py:101-152): score = Kn * (q_rot . code / 8 - 15/16 * sum(q_rot)).
+// The K operand of the MFMA is the 4-bit code itself, as the fp16 bit pattern
+// code (the subnormal code * 2^-24, exact; no table, no multiply), so
+// q_rot . code = acc * 2^24 exactly up to fp32 accumulation; V is decoded
+// as in the default form, through a table of cb_v.
+template <int GS, int L, bool SQK = false>
 __global__ void __launch_bounds__(kThreads, 1)
 decode_stream_kernel(SplitParams p) {
-    if (p.cb_same && !*p.cb_same) return;       // different codebooks: the general kernel runs
+    if (!SQK && p.cb_same && !*p.cb_same) return;   // different codebooks: the general kernel runs
     static_assert(L == 16 || L == 4, "4-bit or 2-bit codes");
+    static_assert(!SQK || L == 16, "score-domain QK: 4-bit K codes");
     __shared__ __align__(16) uint8_t smem[kStreamLds];
     constexpr int S = (L == 16) ? 144 : 80;        // slot bytes
     constexpr int KB = (L == 16) ? 64 : 32;        // code bytes per role
@@ -570,6 +580,15 @@ decode_stream_kernel(SplitParams p) {
     const int start = sp * p.tile_n;
     const int end = min(start + p.tile_n, seq_len);
     const int64_t part_row = ((int64_t)b * p.n_splits + sp) * p.H_q + (int64_t)h * GS;
+    if (SQK && !*p.k_uniform) {
+        // Not the uniform codebook: the output is NaN rather than wrong.
+        if (q4 == 0 && r16 < GS) {
+            p.part_ml[(part_row + r16) * 2 + 0] = __builtin_nanf("");
+            p.part_ml[(part_row + r16) * 2 + 1] = __builtin_nanf("");
+        }
+        for (int i = lane; i < GS * kD; i += 64) p.part_o[part_row * kD + i] = __builtin_nanf("");
+        return;
+    }
     if (start >= end) {
         if (q4 == 0 && r16 < GS) {
             p.part_ml[(part_row + r16) * 2 + 0] = -INFINITY;
@@ -626,12 +645,26 @@ decode_stream_kernel(SplitParams p) {
 #pragma unroll
         for (int s = 0; s < 4; ++s) qb[s] = *reinterpret_cast<const uint4 *>(qg + 8 * s);
     }
+    // -15/16 * sum(q_rot) of this lane's query column (SQK), in fp32.
+    float qsum_neg = 0.0f;
+    if constexpr (SQK) {
+        float a = 0.0f;
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            const uint32_t w[4] = {qb[s].x, qb[s].y, qb[s].z, qb[s].w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) a += h2f((uint16_t)(w[e] & 0xFFFFu)) + h2f((uint16_t)(w[e] >> 16));
+        }
+        a += __shfl_xor(a, 16);
+        a += __shfl_xor(a, 32);
+        qsum_neg = -0.9375f * a;
+    }
     {
         // The codebook goes through LDS first: a global load per table entry
         // would put 32 dependent memory round trips in every thread's
         // prologue.
         __shared__ float cbs[16];
-        if (tid < L) cbs[tid] = p.cb_k[tid];
+        if (tid < L) cbs[tid] = SQK ? p.cb_v[tid] : p.cb_k[tid];
         __syncthreads();
         uint32_t *lut = reinterpret_cast<uint32_t *>(smem);
         for (int i = tid; i < kLut2Bytes / 4; i += kThreads) {
@@ -676,6 +709,7 @@ decode_stream_kernel(SplitParams p) {
         float nk;
         uint32_t vw[4];
         float nv[4];
+        float nki[4];      // SQK: K norms of tokens 4*q4 + i
     };
     auto read_page = [&](PageRegs &r, auto slot) CDA_INLINE {
         constexpr uint32_t so = decltype(slot)::value * kHP;
@@ -692,10 +726,34 @@ decode_stream_kernel(SplitParams p) {
                 r.vw[k] = lds_b32(smem + so, oV[k]);
             else
                 r.vw[k] = *reinterpret_cast<const uint16_t *>(smem + so + oV[k]);
-            r.nv[k] = __uint_as_float(lds_b32(smem + so, oNV[k]));
+            if constexpr (SQK) {
+                const float2 kv = *reinterpret_cast<const float2 *>(smem + so + oNV[k] - 4);
+                r.nki[k] = kv.x;
+                r.nv[k] = kv.y;
+            } else {
+                r.nv[k] = __uint_as_float(lds_b32(smem + so, oNV[k]));
+            }
         }
     };
     auto page_scores = [&](const PageRegs &r) CDA_INLINE -> floatx4 {
+        if constexpr (SQK) {
+            // Byte j of a code word: dims 2j (high nibble), 2j + 1 (low).
+            floatx4 acc = {0.f, 0.f, 0.f, 0.f};
+            const uint32_t w[4] = {r.kq.x, r.kq.y, r.kq.z, r.kq.w};
+#pragma unroll
+            for (int s = 0; s < 4; ++s) {
+                const uint32_t lo = w[s] & 0x0F0F0F0Fu, hi = (w[s] >> 4) & 0x0F0F0F0Fu;
+                uint4 a;
+                a.x = __builtin_amdgcn_perm(lo, hi, 0x0C040C00u);
+                a.y = __builtin_amdgcn_perm(lo, hi, 0x0C050C01u);
+                a.z = __builtin_amdgcn_perm(lo, hi, 0x0C060C02u);
+                a.w = __builtin_amdgcn_perm(lo, hi, 0x0C070C03u);
+                acc = mfma16(a, qb[s], acc);
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[i] = r.nki[i] * fmaf(acc[i], 0x1p21f, qsum_neg);
+            return acc;
+        }
         float2 cv[16];
         if constexpr (L == 16) {
             const uint32_t w[4] = {r.kq.x, r.kq.y, r.kq.z, r.kq.w};
@@ -823,6 +881,7 @@ decode_stream_kernel(SplitParams p) {
                     for (int i = 0; i < 4; ++i) {
                         r[k].vw[i] = 0u;
                         r[k].nv[i] = 0.0f;
+                        r[k].nki[i] = 0.0f;
                     }
                 }
         }
@@ -936,7 +995,8 @@ constexpr int kHeadsPerBlock = 4;
 
 __global__ void __launch_bounds__(256)
 rotate_q_kernel(const uint16_t *q, const float *R, uint16_t *q_rot, int H_q,
-                const float *cb_k, const float *cb_v, int levels, int *cb_same) {
+                const float *cb_k, const float *cb_v, int levels, int *cb_same,
+                int *k_uniform) {
     __shared__ __align__(16) float Rs[kD * kD];
     __shared__ float qs[kHeadsPerBlock][kD];
     const int b = blockIdx.y, t = threadIdx.x;
@@ -946,6 +1006,13 @@ rotate_q_kernel(const uint16_t *q, const float *R, uint16_t *q_rot, int H_q,
         const bool eq = t >= levels || __float_as_uint(cb_k[t]) == __float_as_uint(cb_v[t]);
         const bool all = __builtin_amdgcn_ballot_w64(!eq) == 0;
         if (t == 0) *cb_same = all ? 1 : 0;
+    }
+    if (k_uniform && blockIdx.x == 0 && blockIdx.y == 0 && t >= 64 && t < 128) {
+        // Whether cb_k is the uniform codebook the score-domain QK assumes.
+        const int i = t - 64;
+        const bool eq = i >= 16 || cb_k[i] == (float)(2 * i + 1) * 0.0625f - 1.0f;
+        const bool all = __builtin_amdgcn_ballot_w64(!eq) == 0;
+        if (i == 0) *k_uniform = all ? 1 : 0;
     }
     const int h0 = blockIdx.x * kHeadsPerBlock;
     const float4 *R4 = reinterpret_cast<const float4 *>(R);
@@ -1229,7 +1296,8 @@ int decode_impl(const void *q, const void *kv_cache, int slot_bytes, int H_kv,
                 const float *cb_k, const float *cb_v, int levels_k, int levels_v,
                 const float *rot_f32, void *out, int B, int H_q, int group_size, int block_size,
                 int tile_n, int max_seq_len, float scale, void *workspace,
-                size_t workspace_bytes, void *stream, const char *fn) {
+                size_t workspace_bytes, void *stream, const char *fn,
+                bool uniform_qk = false) {
     const std::string f(fn);
     CDA_REQUIRE(q && kv_cache && block_table && seq_lens && cb_k && cb_v && rot_f32 && out,
                 f + ": null pointer argument");
@@ -1273,10 +1341,15 @@ int decode_impl(const void *q, const void *kv_cache, int slot_bytes, int H_kv,
                               ((levels_k == 16 && slot_bytes == 144) ||
                                (levels_k == 4 && slot_bytes == 80)) &&
                               tn <= 16 * kStreamMaxPages && g_allow_stream;
-    const bool dual = stream_shape && cb_k != cb_v;
+    if (uniform_qk)
+        CDA_REQUIRE(stream_shape && levels_k == 16,
+                    f + ": the score-domain QK runs on the page-streaming kernel: K4V4 "
+                        "144-byte slots, 8 KV heads, splits of at most 16384 tokens");
+    const bool dual = stream_shape && cb_k != cb_v && !uniform_qk;
     int *cb_same = dual ? reinterpret_cast<int *>(ws + w.flag) : nullptr;
+    int *k_uniform = uniform_qk ? reinterpret_cast<int *>(ws + w.flag) + 1 : nullptr;
     rotate_q_kernel<<<head_grid, 256, 0, st>>>(static_cast<const uint16_t *>(q), rot_f32, q_rot,
-                                               H_q, cb_k, cb_v, levels_k, cb_same);
+                                               H_q, cb_k, cb_v, levels_k, cb_same, k_uniform);
     CDA_LAUNCH_CHECK("rotate_q_kernel");
 
     SplitParams p;
@@ -1299,11 +1372,17 @@ int decode_impl(const void *q, const void *kv_cache, int slot_bytes, int H_kv,
     p.scale_log2 = scale * kLog2e;
     p.levels = levels_k;
     p.cb_same = cb_same;
+    p.k_uniform = k_uniform;
     dim3 grid(ns, (H_kv + kWaves - 1) / kWaves, B);
     const bool use_stream = stream_shape;
     if (g_split_start && hipEventRecord(g_split_start, st) != hipSuccess)
         return fail(CDA_E_HIP, f + ": hipEventRecord(start) failed");
-    if (use_stream) {
+    if (uniform_qk) {
+        if (group_size == 4)
+            decode_stream_kernel<4, 16, true><<<grid, kThreads, 0, st>>>(p);
+        else
+            decode_stream_kernel<8, 16, true><<<grid, kThreads, 0, st>>>(p);
+    } else if (use_stream) {
         if (levels_k == 16) {
             if (group_size == 4)
                 decode_stream_kernel<4, 16><<<grid, kThreads, 0, st>>>(p);
@@ -1316,7 +1395,7 @@ int decode_impl(const void *q, const void *kv_cache, int slot_bytes, int H_kv,
                 decode_stream_kernel<8, 4><<<grid, kThreads, 0, st>>>(p);
         }
     }
-    if (!use_stream || dual) {
+    if (!uniform_qk && (!use_stream || dual)) {
         if (levels_k == 4) {
             if (group_size == 4)
                 decode_split_kernel<4, 4, 4><<<grid, kThreads, 0, st>>>(p);
@@ -1366,6 +1445,19 @@ extern "C" int cda_decode_full_hmma_v3(const void *q, const void *kv_cache, int6
                        cb_v, levels, levels, rot_f32, out, B, H_q, group_size, block_size, tile_n,
                        max_seq_len, scale, workspace, workspace_bytes, stream,
                        "cda_decode_full_hmma_v3");
+}
+
+extern "C" int cda_decode_full_hmma_v3_uniform_qk(
+    const void *q, const void *kv_cache, int64_t num_slots, int slot_bytes, int H_kv,
+    const int32_t *block_table, int bt_stride, const int32_t *seq_lens, const float *cb_k,
+    const float *cb_v, const float *rot_f32, void *out, int B, int H_q, int group_size,
+    int block_size, int tile_n, int max_seq_len, float scale, void *workspace,
+    size_t workspace_bytes, void *stream) {
+    (void)num_slots;
+    return decode_impl(q, kv_cache, slot_bytes, H_kv, block_table, bt_stride, seq_lens, cb_k,
+                       cb_v, 16, 16, rot_f32, out, B, H_q, group_size, block_size, tile_n,
+                       max_seq_len, scale, workspace, workspace_bytes, stream,
+                       "cda_decode_full_hmma_v3_uniform_qk", true);
 }
 
 extern "C" int cda_decode_full_hmma_v3_k4v2(const void *q, const void *kv_cache,
