@@ -276,8 +276,10 @@ def prefill_main(args) -> int:
 def prefill_chunk_main(args) -> int:
     """--prefill-chunk: chunked prefill, Q new queries per sequence over K keys
     (the last Q keys are the chunk's own, causal).  Times the compressed-tile
-    kernel with its key split (the default for such chunks), without it, and
-    the dense bridge; one JSON line (not the headline metric)."""
+    kernel with its key split (the default for such chunks), without it, the
+    dense bridge, and the hybrid route (compressed prefix + the chunk's raw
+    fp16 K/V, cda_prefill_hybrid_rawkv); one JSON line (not the headline
+    metric)."""
     import torch
     from sub0_amd import _native
     dev = torch.device("cuda:0")
@@ -294,6 +296,11 @@ def prefill_chunk_main(args) -> int:
                                           block_size=BS, max_seq_len=K)
     cu_k = torch.arange(0, B + 1, dtype=torch.int32, device=dev) * K
     sc = 1.0 / D ** 0.5
+    k_new = torch.randn(B * Qn, H_KV, D, generator=gpu, device=dev, dtype=torch.float16)
+    v_new = torch.randn(B * Qn, H_KV, D, generator=gpu, device=dev, dtype=torch.float16)
+    hws = torch.empty(int(_native.lib().cda_prefill_hybrid_workspace_size(B, B * Qn, H_Q, H_KV,
+                                                                          Qn, K)) + 256,
+                      dtype=torch.uint8, device=dev)
     variants = {
         "split": lambda: _native.prefill_paged(q, w["cache"], w["bt"], cu, w["seq"], w["cb"],
                                                w["cb"], out, block_size=BS, max_query_len=Qn,
@@ -303,6 +310,10 @@ def prefill_chunk_main(args) -> int:
                                                  scale=sc),
         "dense_kernel": lambda: _native.fa2_varlen_fwd_hadamard(q, k_rot, v_rot, out, cu, cu_k,
                                                                 w["seq"], Qn, K, sc),
+        "hybrid": lambda: _native.prefill_hybrid(q, k_new, v_new, w["cache"], w["bt"], cu, w["seq"],
+                                                 w["cb"], w["cb"], out, block_size=BS,
+                                                 max_query_len=Qn, max_seq_len=K, scale=sc,
+                                                 workspace=hws),
     }
     res = {}
     outs = {}
@@ -328,6 +339,8 @@ def prefill_chunk_main(args) -> int:
         "roofline": {"bound": "mfma", "achieved": round(tf, 2), "peak": peak, "unit": "TFLOP/s",
                      "frac": round(tf / peak, 5)},
         "unsplit_us": round(res["unsplit"], 2), "dense_kernel_us": round(res["dense_kernel"], 2),
+        "hybrid_us": round(res["hybrid"], 2),
+        "hybrid_tflops": round(flops / (res["hybrid"] * 1e-6) / 1e12, 2),
         "split_vs_unsplit_max_abs": err,
     }
     print(json.dumps(line), flush=True)

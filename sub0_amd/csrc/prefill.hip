@@ -770,7 +770,6 @@ __global__ void __launch_bounds__(256)
 prefill_combine_kernel(const float *__restrict__ part_o, const float *__restrict__ part_ml,
                        uint16_t *__restrict__ out, int T, int H_q, int n_ksplit,
                        const int32_t *__restrict__ cu_q, int B) {
-    __shared__ float obs[4][kD];
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int hq = blockIdx.y * 4 + wave;
     const int t = blockIdx.x;
@@ -812,21 +811,28 @@ prefill_combine_kernel(const float *__restrict__ part_o, const float *__restrict
         }
     }
     const float inv_l = 1.0f / fmaxf(l, 1e-30f);
-    obs[wave][2 * lane] = (float)(_Float16)(o0 * inv_l);
-    obs[wave][2 * lane + 1] = (float)(_Float16)(o1 * inv_l);
-    __syncthreads();
-    // out[j] = sum_k (-1)^popcount(j & k) O_rot[k] / sqrt(128) (Sylvester order).
-    const int j0 = 2 * lane, j1 = 2 * lane + 1;
-    float a0 = 0.0f, a1 = 0.0f;
-#pragma unroll 8
-    for (int k = 0; k < kD; ++k) {
-        const float x = obs[wave][k];
-        a0 += (__builtin_popcount(j0 & k) & 1) ? -x : x;
-        a1 += (__builtin_popcount(j1 & k) & 1) ? -x : x;
+    // O_rot = fp16(O / l) (attention.py:93), then out = O_rot H / sqrt(128) by
+    // a fast Walsh-Hadamard transform: lane l holds dims 2l, 2l+1; the stage
+    // on index bit 0 runs in registers, bits 1-6 pair lane l with lane
+    // l ^ 2^(b-1) (x_i + x_partner where bit b of i is clear, x_partner - x_i
+    // where it is set): the Sylvester sum sum_k (-1)^popcount(j & k) x_k.
+    float x0 = (float)(_Float16)(o0 * inv_l);
+    float x1 = (float)(_Float16)(o1 * inv_l);
+    {
+        const float a = x0 + x1, b = x0 - x1;
+        x0 = a;
+        x1 = b;
+    }
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        const float p0 = __shfl_xor(x0, d), p1 = __shfl_xor(x1, d);
+        const float sgn = (lane & d) ? -1.0f : 1.0f;
+        x0 = fmaf(sgn, x0, p0);
+        x1 = fmaf(sgn, x1, p1);
     }
     const float hs = 0.08838834764831845f;
     typedef _Float16 half2_ __attribute__((ext_vector_type(2)));
-    const half2_ hv = {(_Float16)(a0 * hs), (_Float16)(a1 * hs)};
+    const half2_ hv = {(_Float16)(x0 * hs), (_Float16)(x1 * hs)};
     *reinterpret_cast<half2_ *>(out + row * kD + 2 * lane) = hv;
 }
 
