@@ -255,8 +255,8 @@ def prefill_main(args) -> int:
                    "lengths": w["lens"], "tokens": w["T"], "flops": w["flops"]},
         "roofline": {"bound": "mfma", "achieved": round(k_tflops, 1), "peak": peak,
                      "unit": "TFLOP/s", "frac": round(k_tflops / peak, 4),
-                     "traffic": load_kernel_traffic("prefill_kernel<dense>" if chosen == "dense"
-                                                    else "prefill_kernel<paged>", "config3"),
+                     **load_kernel_traffic("prefill_kernel<dense>" if chosen == "dense"
+                                           else "prefill_kernel<paged>", "config3"),
                      "kernel": "prefill_kernel<dense>" if chosen == "dense"
                      else "prefill_kernel<paged>", "kernel_ms": round(kernel_ms, 4)},
         "prefill_source": chosen,
@@ -553,7 +553,7 @@ def encode_main(args) -> int:
                    "tokens": w["T"], "algorithmic_bytes": w["bytes"]},
         "roofline": {"bound": "hbm", "achieved": round(k_gbs, 1), "peak": 8000.0, "unit": "GB/s",
                      "frac": round(k_gbs / 8000.0, 4),
-                     "traffic": load_kernel_traffic("paged_encode_kernel<16>", "config2"),
+                     **load_kernel_traffic("paged_encode_kernel<16>", "config2"),
                      "kernel": "paged_encode_kernel<16>", "kernel_us": round(k_us, 2)},
         "k2v2": {"tokens": w2["T"], "algorithmic_bytes": w2["bytes"], "ms_per_step": round(ms2, 5),
                  "value": round(w2["bytes"] / (ms2 * 1e-3) / 1e9, 1),
@@ -978,29 +978,37 @@ def cpu_baseline(threads: int | None = None, reps: int = 5):
 # -------------------------------------------------------------------- main --
 
 def load_kernel_traffic(kernel, workload):
-    """HBM bytes per launch of `kernel` on a named workload (config2, config3)
-    from the committed rocprofv3 PMC summary, or None."""
+    """{"traffic": HBM bytes per launch, "traffic_measured_at": commit} of
+    `kernel` on a named workload (config2, config3) from the committed
+    rocprofv3 PMC summary (None values when absent)."""
+    none = {"traffic": None, "traffic_measured_at": None}
     p = ROOT / "profiles" / "kernel_traffic.json"
     if not p.is_file():
-        return None
+        return none
     try:
         cell = json.loads(p.read_text()).get("kernels", {}).get(kernel, {}).get(workload)
-        return None if cell is None else int(cell["hbm_bytes_per_launch"])
+        if cell is None:
+            return none
+        return {"traffic": int(cell["hbm_bytes_per_launch"]),
+                "traffic_measured_at": cell.get("measured_at")}
     except (ValueError, KeyError, TypeError):
-        return None
+        return none
 
 
 def load_traffic(kernel, B, N):
-    """HBM bytes per launch of `kernel` from the committed rocprofv3 PMC summary."""
+    """(HBM bytes per launch of `kernel`, the commit it was measured at) from
+    the committed rocprofv3 PMC summary, or (None, None)."""
     p = ROOT / "profiles" / "decode_traffic.json"
     if not p.is_file():
-        return None
+        return None, None
     try:
         d = json.loads(p.read_text())
         cell = d.get("kernels", {}).get(kernel, {}).get(f"{B},{N}")
-        return None if cell is None else int(cell["hbm_bytes_per_launch"])
+        if cell is None:
+            return None, None
+        return int(cell["hbm_bytes_per_launch"]), cell.get("measured_at")
     except (ValueError, KeyError, TypeError):
-        return None
+        return None, None
 
 
 def main(argv=None):
@@ -1148,12 +1156,12 @@ def main(argv=None):
     # Both code widths (8 KV heads, one codebook) take the page-streaming kernel
     # unless it is switched off.
     kernel = "decode_split_kernel" if args.general_kernel else "decode_stream_kernel"
-    traffic = (load_traffic(kernel, B, N) if levels == 16 and not args.gs8
-               and not args.uniform_qk else None)
     variant = "K4V4" if levels == 16 else "K2V2"
     if args.uniform_qk:
         variant += " (uniform K codebook, score-domain QK)"
         kernel = "decode_stream_kernel<SQK>"
+    traffic, traffic_at = (load_traffic(kernel, B, N) if levels == 16 and not args.gs8
+                           else (None, None))
     line = {
         "metric": METRIC,
         "value": round(value, 1),
@@ -1179,7 +1187,7 @@ def main(argv=None):
                    "tile_n": tile, "splits": splits, "algorithmic_bytes": nbytes},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / PEAK_GBS, 4),
-                     "traffic": traffic, "kernel": kernel,
+                     "traffic": traffic, "traffic_measured_at": traffic_at, "kernel": kernel,
                      "kernel_us": round(k_us, 2)},
         "cpu_baseline": cpu,
     }
