@@ -530,6 +530,13 @@ __device__ __forceinline__ uint32_t lds_b32(const uint8_t *base, uint32_t off) {
 __host__ __device__ constexpr int vslot(int t) { return (t & 12) | ((t + (t >> 2)) & 3); }
 __host__ __device__ constexpr int vslot_inv(int s) { return (s & 12) | ((s - (s >> 2)) & 3); }
 
+// The score-domain form (SQK) bounds the drift between its waves with a
+// workgroup barrier every 8 chunks: with the lighter K side it is bound by the
+// fetched bytes, and waves that drift apart fetch the 64-byte segments shared
+// by neighbouring heads twice (B=32, N=64K: 495 -> 468 us; every 2, 3, 16
+// chunks 469-482 us).  The exact-dequant form runs slower with any such
+// barrier (its VALU phases would fall into lockstep).
+constexpr int kSqkSyncChunks = 8;
 constexpr int kStreamPages = 4;
 constexpr int kStreamRingOff = kLut2Bytes;
 constexpr int kStreamPidOff = kStreamRingOff + kWaves * kStreamPages * kHeadPage;
@@ -969,7 +976,12 @@ decode_stream_kernel(SplitParams p) {
 
     const int nchunks = (npages + 3) >> 2;
     const int nfull = (end - start) >> 6;
-    for (int c = 0; c < nfull; ++c) step(c, std::false_type{});
+    for (int c = 0; c < nfull; ++c) {
+        step(c, std::false_type{});
+        if constexpr (SQK) {
+            if (c % kSqkSyncChunks == kSqkSyncChunks - 1) __syncthreads();
+        }
+    }
     if (nfull < nchunks) step(nfull, std::true_type{});
 
     const float l = rows_sum(l_run);
