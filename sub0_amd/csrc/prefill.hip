@@ -573,7 +573,8 @@ prefill_kernel(PrefillParams p) {
     }
     __syncthreads();   // tables visible
 
-    for (int j = jt0; j < jt1; ++j) {
+    // Tile j into LDS (the whole workgroup), then the loads of tile j + 1.
+    auto produce = [&](int j) CDA_INLINE {
         uint8_t *buf = smem + (j & 1) * kTileBytes;
         store_tile<PAGED>(cur, buf, buf + kKTile, lutk, lutv, tid);
         if (j + 1 < jt1) {
@@ -582,10 +583,21 @@ prefill_kernel(PrefillParams p) {
             if (j + 2 < jt1) rows_next = fetch_rows<PAGED>(p, bt_row, k2, min(kBN, kend - k2), tid);
         }
         __syncthreads();
-        const int kbase = j * kBN;
-        if (!wave_live || kbase >= wave_kend) continue;
-        if (kbase + kBN <= wave_kfull) tile(buf, kbase, std::false_type{});
-        else tile(buf, kbase, std::true_type{});
+        return buf;
+    };
+    // The tiles whole for every row of this wave come first, those crossing
+    // the causal diagonal or the end of the keys last: two loops (the same
+    // number of barriers for every wave) keep one compute path per loop body,
+    // so the O accumulators stay in the same registers from tile to tile.
+    const int j_mask = __builtin_amdgcn_readfirstlane(
+        wave_live ? max(jt0, min(jt1, wave_kfull / kBN)) : jt1);
+    for (int j = jt0; j < j_mask; ++j) {
+        const uint8_t *buf = produce(j);
+        if (j * kBN < wave_kend) tile(buf, j * kBN, std::false_type{});
+    }
+    for (int j = j_mask; j < jt1; ++j) {
+        const uint8_t *buf = produce(j);
+        if (wave_live && j * kBN < wave_kend) tile(buf, j * kBN, std::true_type{});
     }
     if (!wave_live) return;
 
