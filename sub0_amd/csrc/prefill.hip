@@ -43,8 +43,7 @@ constexpr int kThreads = 64 * kWaves;
 constexpr uint32_t kXcds = 8;            // MI355X: 8 XCDs, each with its own L2
 constexpr float kLog2e = 1.4426950408889634f;
 
-// LDS: two tile buffers, then the code-byte dequant tables (paged source),
-// then the q_rot operands.
+// LDS: two tile buffers, then the code-byte dequant tables (paged source).
 //   K tile   [64 keys][128 dims] fp16, natural dim order, rows padded to 272 B.
 //   V^T tile [128 dims][64 keys] fp16, rows padded to 144 B; within each
 //            16-key group the keys are stored in the MFMA k order (key
@@ -63,10 +62,9 @@ constexpr int kLutOff = 2 * kTileBytes;
 // interleaved copies measured the same).
 constexpr int kLutEntry = 8;                           // bytes per code byte
 constexpr int kLutBytes = 2 * 256 * kLutEntry;         // 4 KiB
-// q_rot operands parked in LDS (8 x 16 bytes per lane per wave) instead of
-// registers: the key loop needs the registers more than the LDS bandwidth.
-constexpr int kQOff = kLutOff + kLutBytes;
-constexpr int kPrefillLds = kQOff + kWaves * 8 * 64 * 16;
+// The q_rot operands stay in registers (8 x 16 bytes per lane): reading them
+// from LDS every tile cost 2-3 % (dense / compressed kernel, config 3).
+constexpr int kPrefillLds = kLutOff + kLutBytes;
 
 __device__ __forceinline__ floatx16 mfma32(half8 a, half8 b, floatx16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
@@ -466,10 +464,6 @@ prefill_kernel(PrefillParams p) {
             qb[S] = __builtin_bit_cast(half8, w);
         }
     }
-    const uint8_t *qlds = smem + kQOff + (uint32_t)wave * (8 * 64 * 16) + (uint32_t)lane * 16;
-#pragma unroll
-    for (int S = 0; S < 8; ++S)
-        *reinterpret_cast<half8 *>(const_cast<uint8_t *>(qlds) + S * 64 * 16) = qb[S];
     // Whole 64-key tile per softmax step: S^T of both 32-key halves (each q
     // operand read once for both), one running-max update, then O^T += V^T P^T.
     // The max is taken on raw scores (the scale is positive: a negative scale
@@ -487,7 +481,7 @@ prefill_kernel(PrefillParams p) {
 #pragma unroll
             for (int i = 0; i < 2; ++i) {
                 const int S = S0 + i;
-                qv[i] = *reinterpret_cast<const half8 *>(qlds + S * 64 * 16);
+                qv[i] = qb[S];
                 a0[i] = *reinterpret_cast<const half8 *>(buf + k_lane + 32 * S);
                 a1[i] = *reinterpret_cast<const half8 *>(buf + k_lane + 32 * kKRow + 32 * S);
             }
