@@ -252,7 +252,8 @@ int cda_prefill_paged_hadamard_ws(const void *q, const void *kv_cache, int64_t n
  * [cu_seqlens_q[b], cu_seqlens_q[b+1]) (causal), in one softmax: the chunk's K
  * and V are rotated to fp16(x H / sqrt(128)) (fa2_cda.py:256-287), each source
  * writes split partials (O, m, l), and the merge (attention.py:239-272) rounds
- * O_rot to fp16 and applies the inverse rotation.
+ * O_rot to fp16 and applies the inverse rotation (when neither side needs a
+ * key split, the prefix kernel merges the chunk's partial in its epilogue).
  *   q, out:         (T, H_q, 128) fp16, unrotated
  *   k_new, v_new:   (T, H_kv, 128) fp16, unrotated, contiguous
  *   kv_cache:       K4V4 paged cache (levels 16)

@@ -178,6 +178,10 @@ struct PrefillParams {
     int ks_base;                // partial slot of split 0 (several sources merged)
     float *part_o;              // (slots, T, H_q, 128) fp32
     float *part_ml;             // (slots, T, H_q, 2): m (log2 domain), l
+    // Unsplit kernel only: when set, slot 0 of part_o / part_ml holds a
+    // partial over other keys of the same queries (written by an earlier
+    // launch), merged in before the epilogue (attention.py:239-272).
+    int merge_slot0;
 };
 constexpr int kKeysAll = 0, kKeysPast = 1, kKeysChunk = 2;
 
@@ -612,6 +616,32 @@ prefill_kernel(PrefillParams p) {
             if (u == 0) *reinterpret_cast<float2 *>(p.part_ml + row * 2) = make_float2(m_run, l_run);
         }
         return;
+    }
+
+    if (p.merge_slot0) {
+        // Merge the partial of the other keys (same lane layout as the split
+        // kernel's partial store): m = max(m1, m2), O = sum 2^(mi - m) Oi.
+        const bool valid = qw0 + c32 < seq_q && q_begin + qw0 + c32 < p.T_total;
+        const int64_t row = (int64_t)(q_begin + min(qw0 + c32, seq_q - 1)) * p.H_q + hq;
+        const float2 ml = valid ? *reinterpret_cast<const float2 *>(p.part_ml + row * 2)
+                                : make_float2(-INFINITY, 0.0f);
+        const float m = fmaxf(m_run, ml.x);
+        const float a = (m_run == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(m_run - m);
+        const float c = (ml.x == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(ml.x - m);
+        l_run = l_run * a + ml.y * c;
+        m_run = m;
+        const float *po = p.part_o + row * kD;
+#pragma unroll
+        for (int T = 0; T < 4; ++T)
+#pragma unroll
+            for (int gi = 0; gi < 4; ++gi) {
+                const float4 v = valid ? *reinterpret_cast<const float4 *>(po + 32 * T + 8 * gi + 4 * u)
+                                       : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                o[T][4 * gi + 0] = fmaf(o[T][4 * gi + 0], a, v.x * c);
+                o[T][4 * gi + 1] = fmaf(o[T][4 * gi + 1], a, v.y * c);
+                o[T][4 * gi + 2] = fmaf(o[T][4 * gi + 2], a, v.z * c);
+                o[T][4 * gi + 3] = fmaf(o[T][4 * gi + 3], a, v.w * c);
+            }
     }
 
     // ---- epilogue: O_rot = fp16(O / l) (attention.py:93), out = fp16(O_rot H / sqrt(128)).
@@ -1259,6 +1289,9 @@ extern "C" int cda_hadamard128_fp16(const void *x, void *y, int64_t rows, float 
 //   2. the paged kernel over the prefix writes partials to slots [0, nA);
 //   3. the dense kernel over the rotated chunk writes slots [nA, nA + nB);
 //   4. prefill_combine_kernel merges the nA + nB slots and unrotates.
+// When neither side needs a key split (nA = nB = 1) the chunk's partial goes
+// to slot 0 first and the unsplit prefix kernel merges it before its own
+// epilogue: no prefix partials, no combine launch.
 // Workspace: the partials, then the rotated chunk K and V.
 // ---------------------------------------------------------------------------
 namespace cda {
@@ -1359,6 +1392,25 @@ extern "C" int cda_prefill_hybrid_rawkv(const void *q, const void *k_new, const 
     p.part_o = reinterpret_cast<float *>(ws);
     p.part_ml = reinterpret_cast<float *>(
         ws + (((size_t)(h.na + h.nb) * T * H_q * cda::kD * 4 + 255) & ~(size_t)255));
+    if (h.na == 1 && h.nb == 1) {
+        // No key split on either side: the chunk's keys go to partial slot 0,
+        // then the unsplit prefix kernel merges that slot into its own result
+        // before the epilogue (no prefix partials, no combine launch).
+        p.causal = 1;
+        p.key_range = kKeysChunk;
+        p.ks_base = 0;
+        p.n_ksplit = 1;
+        p.ksplit_tiles = h.nb_tiles;
+        p.k_rot = k_rot;
+        p.v_rot = v_rot;
+        p.cu_k = cu_seqlens_q;
+        int rc = launch_prefill_kernel<false>(p, B, max_query_len, true, st, fn);
+        if (rc != CDA_OK) return rc;
+        p.causal = 0;
+        p.key_range = kKeysPast;
+        p.merge_slot0 = 1;
+        return launch_prefill_kernel<true>(p, B, max_query_len, false, st, fn);
+    }
     // The compressed prefix: every key precedes every query of the chunk.
     p.causal = 0;
     p.key_range = kKeysPast;

@@ -33,6 +33,9 @@ CASES = [
     ("big_chunk", [600], [700], 8, 4),
     ("gs8", [70, 33], [150, 33], 4, 8),
     ("hkv2", [129], [1000], 2, 4),
+    # >= 256 workgroups on both sides: no key split, the prefix kernel merges
+    # the chunk's partial in its epilogue (no combine launch)
+    ("no_split_merge", [1024, 1040], [2048, 1500], 8, 4),
 ]
 
 
