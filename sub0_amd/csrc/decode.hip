@@ -633,9 +633,8 @@ decode_stream_kernel(SplitParams p) {
         }
     }
     const uint8_t *kv_h = p.kv + h * S;
-    // DMA of page t into ring slot k.
-    auto issue = [&](int t, int k) CDA_INLINE {
-        const int64_t row0 = __builtin_amdgcn_readfirstlane(page_row[t]);
+    // DMA of the page starting at cache row row0 into ring slot k.
+    auto issue_row = [&](int64_t row0, int k) CDA_INLINE {
         const uint64_t base = (uint64_t)(kv_h + row0 * kRow);
         const v4u32 r = {(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)base),
                          (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(base >> 32) & 0xFFFFu),
@@ -645,6 +644,21 @@ decode_stream_kernel(SplitParams p) {
         if constexpr (L == 16) dma_page_chunk(r, src[1], sb + kVo);
         if (lane < 16) dma_page_chunk(r, src[2], sb + kNo);
     };
+    // DMA of page t (row from the workgroup's table) into ring slot k.
+    auto issue = [&](int t, int k) CDA_INLINE {
+        issue_row(__builtin_amdgcn_readfirstlane(page_row[t]), k);
+    };
+    // The first chunk's pages straight from the block table (wave-uniform
+    // loads), before the tables are built: their latency overlaps the set-up.
+    {
+        const int32_t *bt = p.block_table + (int64_t)b * p.bt_stride;
+#pragma unroll
+        for (int k = 0; k < kStreamPages; ++k)
+            if (k < npages) {
+                const int t0 = start + 16 * k;
+                issue_row((int64_t)__builtin_amdgcn_readfirstlane(bt[t0 / bs]) * bs + t0 % bs, k);
+            }
+    }
     uint4 qb[4];
     {
         const uint16_t *qg =
@@ -684,10 +698,6 @@ decode_stream_kernel(SplitParams p) {
     }
     __syncthreads();
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-
-#pragma unroll
-    for (int k = 0; k < kStreamPages; ++k)
-        if (k < npages) issue(k, k);
 
     const uint32_t rb0 = (uint32_t)(kStreamRingOff + wave * (kStreamPages * kHP));
     // K4V4: token r16's 16 code bytes of dims [32*q4, +32); K2V2: its 8 bytes.
