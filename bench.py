@@ -50,11 +50,12 @@ def log(*a):
 # --------------------------------------------------------------- workload --
 
 def make_workload(B: int, N: int, dev, seed: int | None = None, identity_bt: bool = False,
-                  levels: int = 16, k_uniform: bool = False):
-    """Paged K4V4 (levels 16, 144-byte slots) or K2V2 (levels 4, 80-byte
-    slots) cache of B sequences x N tokens, encoded on the GPU by the fused
-    encoder from K, V ~ N(0,1) fp16 (K with 4 seeded outlier channels x8),
-    plus q ~ N(0,1); synthetic data."""
+                  levels: int = 16, k_uniform: bool = False, k4v2: bool = False):
+    """Paged K4V4 (levels 16, 144-byte slots), K2V2 (levels 4, 80-byte slots)
+    or legacy K4V2 (k4v2: 16-level K, 4-level V, 104-byte slots) cache of B
+    sequences x N tokens, encoded on the GPU by the fused encoder from
+    K, V ~ N(0,1) fp16 (K with 4 seeded outlier channels x8), plus
+    q ~ N(0,1); synthetic data."""
     import torch
     from sub0_amd import _native
     from sub0_amd.cda.algorithm.compression import hadamard_matrix, lloyd_max_centroids_beta
@@ -66,12 +67,13 @@ def make_workload(B: int, N: int, dev, seed: int | None = None, identity_bt: boo
     perm = torch.arange(B * nb) if identity_bt else torch.randperm(B * nb, generator=cpu)
     bt = perm.to(torch.int32).view(B, nb).to(dev)
     outl = torch.randperm(D, generator=cpu)[:4].to(dev)
-    cache = torch.zeros(B * nb * BS, H_KV, 144 if levels == 16 else 80, dtype=torch.uint8,
-                        device=dev)
+    slot = 104 if k4v2 else (144 if levels == 16 else 80)
+    cache = torch.zeros(B * nb * BS, H_KV, slot, dtype=torch.uint8, device=dev)
     cb = lloyd_max_centroids_beta(levels, D).to(dev)
     # k_uniform: K codes from the uniform codebook (the score-domain QK option)
     from sub0_amd.cda.algorithm.compression import uniform_centroids
     cbk = uniform_centroids(levels).to(dev) if k_uniform else cb
+    cbv = lloyd_max_centroids_beta(4, D).to(dev) if k4v2 else cb
     chunk = 1 << 16                                    # tokens per encode launch
     pos = torch.arange(N, device=dev, dtype=torch.int64)
     for b in range(B):
@@ -81,12 +83,12 @@ def make_workload(B: int, N: int, dev, seed: int | None = None, identity_bt: boo
             k = torch.randn(t1 - t0, H_KV, D, generator=gpu, device=dev, dtype=torch.float16)
             k[..., outl] *= 8
             v = torch.randn(t1 - t0, H_KV, D, generator=gpu, device=dev, dtype=torch.float16)
-            _native.paged_encode(k, v, slots_b[t0:t1].contiguous(), cache, cbk, cb)
+            _native.paged_encode(k, v, slots_b[t0:t1].contiguous(), cache, cbk, cbv)
     q = torch.randn(B, H_Q, D, generator=gpu, device=dev, dtype=torch.float16)
     seq = torch.full((B,), N, dtype=torch.int32, device=dev)
     R = hadamard_matrix(D).to(dev)
     torch.cuda.synchronize()
-    return dict(q=q, cache=cache, bt=bt, seq=seq, cb=cb, cbk=cbk, R=R, R16=R.half(),
+    return dict(q=q, cache=cache, bt=bt, seq=seq, cb=cb, cbk=cbk, cbv=cbv, R=R, R16=R.half(),
                 out=torch.empty_like(q), B=B, N=N, uniform_qk=k_uniform)
 
 
@@ -810,7 +812,7 @@ def decode_call(w, tile_n: int = 0):
 
     def call():
         decode_hmma_v1(w["q"], w["cache"], w["bt"], w["seq"], w["out"], cb_K=w["cbk"],
-                       cb_V=w["cb"], rotation_fp32=w["R"], rotation_fp16=w["R16"],
+                       cb_V=w["cbv"], rotation_fp32=w["R"], rotation_fp16=w["R16"],
                        group_size=H_Q // H_KV, block_size=BS, max_seq_len=w["N"],
                        qk_without_k_decode=w["uniform_qk"])
     return call
@@ -1046,6 +1048,9 @@ def main(argv=None):
     ap.add_argument("--uniform-qk", action="store_true",
                     help="decode a cache with the uniform 16-level K codebook through the "
                          "score-domain QK option (attention.py:101-187)")
+    ap.add_argument("--k4v2", action="store_true",
+                    help="decode the legacy K4V2 cache (16-level K, 4-level V, 104-byte slots; "
+                         "the general split kernel)")
     ap.add_argument("--k2v2", action="store_true",
                     help="decode over a K2V2 cache (4-level codebook, 80-byte slots) instead of K4V4")
     ap.add_argument("--general-kernel", action="store_true",
@@ -1094,7 +1099,7 @@ def main(argv=None):
         H_Q = 8 * H_KV
     levels = 4 if args.k2v2 else 16
     w = make_workload(B, N, dev, identity_bt=args.identity_block_table, levels=levels,
-                      k_uniform=args.uniform_qk)
+                      k_uniform=args.uniform_qk, k4v2=args.k4v2)
     fn = decode_call(w, args.tile_n)
     g = capture(fn, args.warmup)
     settle(g)
@@ -1109,7 +1114,7 @@ def main(argv=None):
     ms_per_step = (t1 - t0) / args.steps * 1e3
     med_us = replay_median_us(g, 20)
     k_us = split_kernel_us(fn, max(5, args.steps))
-    slot_data = 136 if levels == 16 else 72
+    slot_data = 104 if args.k4v2 else (136 if levels == 16 else 72)
     nbytes = _native.decode_algorithmic_bytes(B, N, H_q=H_Q, slot_data=slot_data)
     value = nbytes / (ms_per_step * 1e-3) / 1e9
     achieved = nbytes / (k_us * 1e-6) / 1e9
@@ -1145,7 +1150,8 @@ def main(argv=None):
 
     cpu = None
     # the CPU baseline is config 0 (K4V4, 32 Q heads)
-    if not args.no_cpu_baseline and levels == 16 and not args.gs8 and not args.uniform_qk:
+    if (not args.no_cpu_baseline and levels == 16 and not args.gs8 and not args.uniform_qk
+            and not args.k4v2):
         try:
             cpu = cpu_baseline()
         except Exception as e:  # the baseline is reported, never required
@@ -1157,11 +1163,14 @@ def main(argv=None):
     # unless it is switched off.
     kernel = "decode_split_kernel" if args.general_kernel else "decode_stream_kernel"
     variant = "K4V4" if levels == 16 else "K2V2"
+    if args.k4v2:
+        variant = "K4V2 (104-byte slots)"
+        kernel = "decode_split_kernel"
     if args.uniform_qk:
         variant += " (uniform K codebook, score-domain QK)"
         kernel = "decode_stream_kernel<SQK>"
-    traffic, traffic_at = (load_traffic(kernel, B, N) if levels == 16 and not args.gs8
-                           else (None, None))
+    traffic, traffic_at = (load_traffic(kernel, B, N)
+                           if levels == 16 and not args.gs8 and not args.k4v2 else (None, None))
     line = {
         "metric": METRIC,
         "value": round(value, 1),
@@ -1176,7 +1185,8 @@ def main(argv=None):
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": f"u{2 if levels == 4 else 4} codes, fp16 MFMA operands, fp32 accumulate",
+        "dtype": ("u4 K / u2 V codes" if args.k4v2 else f"u{2 if levels == 4 else 4} codes")
+                 + ", fp16 MFMA operands, fp32 accumulate",
         "data": "synthetic (K,V,q ~ N(0,1) fp16, K with 4 outlier channels x8, "
                 f"Lloyd-beta {levels}-level codebook, permuted block table)",
         "config": {"workload": f"{variant} paged decode, B={B}, N={N}, "
