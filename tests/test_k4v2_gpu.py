@@ -96,3 +96,28 @@ def test_k4v2_decode_and_loader(gpu, codebooks, seq_lens, H_kv, gs):
                                   O.decode_rotated(c["vp"][b, h, :n], c["vn"][b, h, :n],
                                                    c["cbv"]).view(np.uint16))
         assert not kr[b * N + n:(b + 1) * N].any()
+
+
+def test_k4v2_prefill_through_the_dense_bridge(gpu, codebooks):
+    """fa2_cda_prefill_varlen_v1(k4v2=True): the K4V2 cache dequantised by the
+    K4V2 loader, then the fused attention kernel (fa2_cda.py:98-230 with the
+    k4v2 loader of :64-95); against the checker's causal prefill on the same
+    cache, 2e-3."""
+    from sub0_amd.cda.kernels_cuda.fa2_cda import fa2_cda_prefill_varlen_v1
+    seq = [300, 77]
+    print(f"[k4v2] prefill seq={seq}", flush=True)
+    c = _case(930, seq, 8, 4, codebooks)
+    cu = np.concatenate([[0], np.cumsum(seq)]).astype(np.int32)
+    q = synth.normal_f16(933, (int(cu[-1]), 32, 128))
+    exp = O.prefill_paged(q, cu, c["cache"], c["bt"], c["sl"], c["cbk"], c["cbv"], O.hadamard128(),
+                          H_kv=8, block_size=c["bs"])
+    qd = _t(q, gpu)
+    out = torch.full_like(qd, float("nan"))
+    fa2_cda_prefill_varlen_v1(qd, _t(c["cache"], gpu), _t(c["bt"], gpu), _t(cu, gpu),
+                              _t(c["sl"], gpu), out, cb_K=_t(c["cbk"], gpu), cb_V=_t(c["cbv"], gpu),
+                              rotation_fp32=_t(O.hadamard128(), gpu), group_size=4,
+                              block_size=c["bs"], max_query_len=300, max_seq_len=300, k4v2=True)
+    torch.cuda.synchronize()
+    o = out.cpu().numpy()
+    assert np.isfinite(o).all()
+    assert np.abs(o.astype(np.float32) - exp.astype(np.float32)).max() <= TOL
