@@ -34,6 +34,7 @@ namespace cda {
 namespace {
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half2 __attribute__((ext_vector_type(2)));
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 
 constexpr int kD = 128;
@@ -236,15 +237,18 @@ __device__ __forceinline__ void load_tile(const PrefillParams &p, TileRegs &r, T
         r.k[0] = r.k[1] = 0u;
         r.nk = 0.0f;
         if (tk < nk_valid) {
+            // Slot rows and row_bytes are below 2^32 and 2^31: one 32 x 32 -> 64-bit multiply.
             const uint8_t *rp =
-                kvh + ((int64_t)rows.bk * p.block_size + in_block(kbase + tk)) * p.row_bytes;
+                kvh + (uint64_t)(uint32_t)(rows.bk * p.block_size + in_block(kbase + tk)) *
+                          (uint32_t)p.row_bytes;
             const uint2 w = *reinterpret_cast<const uint2 *>(rp + 8 * ck);
             r.k[0] = w.x;
             r.k[1] = w.y;
             r.nk = *reinterpret_cast<const float *>(rp + 128);
         }
         const uint8_t *vp =
-            kvh + ((int64_t)rows.bv * p.block_size + in_block(kbase + 4 * gv)) * p.row_bytes;
+            kvh + (uint64_t)(uint32_t)(rows.bv * p.block_size + in_block(kbase + 4 * gv)) *
+                      (uint32_t)p.row_bytes;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             r.v[i] = 0u;
@@ -256,22 +260,23 @@ __device__ __forceinline__ void load_tile(const PrefillParams &p, TileRegs &r, T
             }
         }
     } else {
-        const int64_t r0 = dense_row0 + kbase;
-        const int64_t hs = (int64_t)p.H_kv * kD;
+        // Dense rows and the row pitch are below 2^31: 32 x 32 -> 64-bit multiplies.
+        const uint32_t r0 = (uint32_t)(dense_row0 + kbase);
+        const uint32_t hs = (uint32_t)(p.H_kv * kD);
         uint4 x0 = make_uint4(0, 0, 0, 0), x1 = x0;
         if (tk < nk_valid) {
             const uint4 *src =
-                reinterpret_cast<const uint4 *>(p.k_rot + (r0 + tk) * hs + h * kD + 16 * ck);
+                reinterpret_cast<const uint4 *>(p.k_rot + (uint64_t)(r0 + tk) * hs + h * kD + 16 * ck);
             x0 = src[0];
             x1 = src[1];
         }
         r.k[0] = x0.x; r.k[1] = x0.y; r.k[2] = x0.z; r.k[3] = x0.w;
         r.k[4] = x1.x; r.k[5] = x1.y; r.k[6] = x1.z; r.k[7] = x1.w;
-        const uint16_t *vrow = p.v_rot + (r0 + 4 * gv) * hs + h * kD + 4 * cv;
+        const uint16_t *vrow = p.v_rot + (uint64_t)(r0 + 4 * gv) * hs + h * kD + 4 * cv;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             uint2 v = make_uint2(0u, 0u);
-            if (4 * gv + i < nk_valid) v = *reinterpret_cast<const uint2 *>(vrow + i * hs);
+            if (4 * gv + i < nk_valid) v = *reinterpret_cast<const uint2 *>(vrow + (size_t)i * hs);
             r.v[2 * i] = v.x;
             r.v[2 * i + 1] = v.y;
         }
@@ -526,7 +531,6 @@ prefill_kernel(PrefillParams p) {
                 for (int r = 0; r < 16; ++r) o[T][r] *= alpha;
         }
         const float m_sub = (m_run == -INFINITY) ? 0.0f : m_run;
-        float ls = 0.0f;
 #pragma unroll
         for (int sub = 0; sub < 2; ++sub)
 #pragma unroll
@@ -534,12 +538,23 @@ prefill_kernel(PrefillParams p) {
                 float e = __builtin_amdgcn_exp2f(fmaf(st[sub][r], scl, -m_sub));
                 if (MASK && st[sub][r] == -INFINITY) e = 0.0f;
                 st[sub][r] = e;
-                ls += e;
             }
+        // P as the fp16 operand of O^T += V^T P^T; the row sum l is taken over
+        // the same rounded values (v_dot2_f32_f16 against ones), per lane: the
+        // two halves of a query's keys are added once after the key loop.
+        half8 pbs[4];
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) pbs[ks] = pack8(st[ks >> 1], 8 * (ks & 1));
         {
-            auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(ls), __float_as_uint(ls),
-                                                       false, false);
-            l_run += __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
+            const half2 one = {(_Float16)1.0f, (_Float16)1.0f};
+            float ls = 0.0f;
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    ls = __builtin_amdgcn_fdot2(half2{pbs[ks][2 * i], pbs[ks][2 * i + 1]}, one, ls,
+                                                false);
+            l_run += ls;
         }
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) {
@@ -547,7 +562,7 @@ prefill_kernel(PrefillParams p) {
 #pragma unroll
             for (int T = 0; T < 4; ++T)
                 a[T] = *reinterpret_cast<const half8 *>(buf + v_lane + T * 32 * kVRow + 32 * ks);
-            const half8 pb = pack8(st[ks >> 1], 8 * (ks & 1));
+            const half8 pb = pbs[ks];
 #pragma unroll
             for (int T = 0; T < 4; ++T) o[T] = mfma32(a[T], pb, o[T]);
         }
@@ -598,6 +613,12 @@ prefill_kernel(PrefillParams p) {
         if (wave_live && j * kBN < wave_kend) tile(buf, j * kBN, std::true_type{});
     }
     if (!wave_live) return;
+    {
+        // l over all of the query's keys: this lane's half plus the partner's.
+        auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(l_run), __float_as_uint(l_run),
+                                                   false, false);
+        l_run = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
+    }
 
     if (KSPLIT) {
         // Partial of this split: O^T rows are dims (acc element i of tile T is
