@@ -74,9 +74,11 @@ class PrefillCase:
     H_kv: int
     block_size: int
     expected: np.ndarray     # oracle output (T, H_q, 128) fp16
+    cb_v: np.ndarray = None  # V codebook when it differs from cb
 
 
-def make_prefill_case(seed, seq_q, seq_k, *, H_kv=8, gs=4, block_size=16, scale=None, fill=0):
+def make_prefill_case(seed, seq_q, seq_k, *, H_kv=8, gs=4, block_size=16, scale=None, fill=0,
+                      cb_v=None):
     """Seeded K/V for each sequence's seq_k keys (encoded by the checker into a
     paged cache), queries for its last seq_q positions, and the checker's
     causal prefill output."""
@@ -90,16 +92,17 @@ def make_prefill_case(seed, seq_q, seq_k, *, H_kv=8, gs=4, block_size=16, scale=
     bt = synth.permuted_block_table(seed, B, W)
     k = synth.kv_with_outliers(seed, (B, H_kv, nmax, D))
     v = synth.normal_f16(seed + 1, (B, H_kv, nmax, D))
+    cbv = cb if cb_v is None else np.asarray(cb_v, dtype=np.float32)
     kp, kn, _ = O.encode(k, cb)
-    vp, vn, _ = O.encode(v, cb)
+    vp, vn, _ = O.encode(v, cbv)
     cache = O.build_paged_cache(kp, kn, vp, vn, bt, block_size, cb.size,
                                 num_blocks=B * W, fill=fill)
     cu = np.concatenate([[0], np.cumsum(seq_q)]).astype(np.int32)
     q = synth.normal_f16(seed + 2, (int(cu[-1]), H_q, D))
     R = O.hadamard128()
-    exp = O.prefill_paged(q, cu, cache, bt, seq_k, cb, cb, R, H_kv=H_kv,
+    exp = O.prefill_paged(q, cu, cache, bt, seq_k, cb, cbv, R, H_kv=H_kv,
                           block_size=block_size, scale=scale)
-    return PrefillCase(q, cu, cache, bt, seq_k, cb, H_kv, block_size, exp)
+    return PrefillCase(q, cu, cache, bt, seq_k, cb, H_kv, block_size, exp, cb_v)
 
 
 @dataclass

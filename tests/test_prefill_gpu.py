@@ -32,16 +32,17 @@ def run_prefill(case, dev, *, dense=False, scale=None, split=False, max_seq_len=
     cu = _dev(case.cu_q, dev)
     sk = _dev(case.seq_k, dev)
     cb = _dev(case.cb, dev)
+    cbv = cb if case.cb_v is None else _dev(case.cb_v, dev)
     sc = scale if scale is not None else 1.0 / np.sqrt(128)
     max_q = int(np.diff(case.cu_q).max()) if len(case.cu_q) > 1 else 0
     max_k = int(case.seq_k.max())
     if dense:
-        k_rot, v_rot = _native.paged_to_dense(cache, bt, sk, cb, cb, block_size=case.block_size,
+        k_rot, v_rot = _native.paged_to_dense(cache, bt, sk, cb, cbv, block_size=case.block_size,
                                               max_seq_len=max_k)
         cu_k = torch.arange(0, len(case.seq_k) + 1, dtype=torch.int32, device=dev) * max_k
         _native.fa2_varlen_fwd_hadamard(q, k_rot, v_rot, out, cu, cu_k, sk, max_q, max_k, sc)
     else:
-        _native.prefill_paged(q, cache, bt, cu, sk, cb, cb, out, block_size=case.block_size,
+        _native.prefill_paged(q, cache, bt, cu, sk, cb, cbv, out, block_size=case.block_size,
                               max_query_len=max_q, scale=sc,
                               max_seq_len=(max_seq_len or max_k) if split else None)
     torch.cuda.synchronize()
@@ -73,6 +74,26 @@ def test_prefill_matches_checker(gpu, name, seq_q, seq_k, H_kv, gs, dense):
     case = make_prefill_case(4000 + len(name), seq_q, seq_k, H_kv=H_kv, gs=gs, fill=0xFF)
     out = run_prefill(case, gpu, dense=dense)
     check(out, case.expected)
+
+
+@pytest.mark.parametrize("split", [False, True], ids=["unsplit", "key_split"])
+@pytest.mark.parametrize("copy", [False, True], ids=["different", "equal_copy"])
+def test_prefill_separate_codebooks(gpu, split, copy):
+    """V encoded with its own codebook (uniform 16 levels), or a separate
+    tensor with the K codebook's values: the compressed-tile kernel builds one
+    shared table or two half tables."""
+    print(f"[prefill] separate codebooks split={split} copy={copy}", flush=True)
+    cbv = synth_cb_copy() if copy else O.uniform_centroids(16)
+    case = make_prefill_case(4600 + 2 * split + copy, [16, 150] if split else [130, 64],
+                             [3000, 1700] if split else [300, 64], H_kv=8, gs=4, fill=0xFF,
+                             cb_v=cbv)
+    check(run_prefill(case, gpu, split=split), case.expected)
+    check(run_prefill(case, gpu, dense=True), case.expected)
+
+
+def synth_cb_copy():
+    from tests.cases import synth_cb
+    return synth_cb().copy()
 
 
 @pytest.mark.parametrize("dense", [False, True], ids=["paged", "dense"])
