@@ -53,6 +53,28 @@ def test_decode_fullsize_against_torch(gpu, stream):
     assert err <= TOL
 
 
+@pytest.mark.parametrize("B,N", [(2, 131072), (1, 262144)], ids=["B2_N128K", "B1_N256K"])
+def test_decode_long_context_against_torch(gpu, B, N):
+    """Contexts past the metric grid: 128K (the reference's longest
+    throughput cell, Fig. 2 / Table A3) and 256K tokens per sequence, through
+    the page-streaming kernel with the default split plan."""
+    import bench
+    from sub0_amd import _native
+    print(f"[fullsize] decode B={B} N={N}", flush=True)
+    w = bench.make_workload(B, N, gpu)
+    k_rot, v_rot = _native.paged_to_dense(w["cache"], w["bt"], w["seq"], w["cb"], w["cb"],
+                                          block_size=BS, max_seq_len=w["N"])
+    ref = _decode_reference(w, k_rot, v_rot)
+    del k_rot, v_rot
+    bench.decode_call(w)()
+    torch.cuda.synchronize()
+    out = w["out"]
+    assert torch.isfinite(out).all()
+    err = (out.float() - ref.float()).abs().max().item()
+    print(f"[fullsize] decode B={B} N={N} max abs err {err:.3e}", flush=True)
+    assert err <= TOL
+
+
 def _k2v2_dense(w, b):
     """Rows of sequence b of a K2V2 cache (80-byte slots: 32 K code bytes, 32 V
     code bytes, fp32 Kn, fp32 Vn) decoded as fp16(centroid * norm), dim 4j in
