@@ -927,37 +927,20 @@ decode_stream_kernel(SplitParams p) {
         cmax = max3f(cmax, max3f(raw[2][1], raw[2][2], raw[2][3]),
                      max3f(raw[3][0], raw[3][1], max3f(raw[3][2], raw[3][3], raw[3][3])));
         cmax = rows_max(cmax);
-        const float m_new = fmaxf(m_run, cmax * p.scale_log2);
-        const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
-        m_run = m_new;
-        float pv[4][4];
-        float psum = 0.0f;
+        // Lazy running max (log2 domain): it moves only when a chunk's max
+        // exceeds it by more than 8, so P <= 2^8 (exact enough in fp16, far
+        // from its range) and the O rescale below is skipped by the whole
+        // wave on almost every chunk.
+        const float cm = cmax * p.scale_log2;
+        const bool move = cm > m_run + 8.0f;
+        if (__builtin_amdgcn_ballot_w64(move)) {
+            const float alpha = move ? __builtin_amdgcn_exp2f(m_run - cm) : 1.0f;  // -inf -> 0
+            m_run = move ? cm : m_run;
+            l_run *= alpha;
+            float al[GS];
 #pragma unroll
-        for (int k = 0; k < 4; ++k)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const float pr = __builtin_amdgcn_exp2f(fmaf(raw[k][i], p.scale_log2, -m_new));
-                psum += pr;
-                pv[k][i] = (MASK && c0 + 16 * k + 4 * q4 + i >= end) ? 0.0f : pr;
-            }
-        l_run = fmaf(l_run, alpha, psum);
-        uint4 pa0, pa1;
-        pa0.x = cvt_pk_rn(pv[0][0], pv[0][1]);
-        pa0.y = cvt_pk_rn(pv[0][2], pv[0][3]);
-        pa0.z = cvt_pk_rn(pv[1][0], pv[1][1]);
-        pa0.w = cvt_pk_rn(pv[1][2], pv[1][3]);
-        pa1.x = cvt_pk_rn(pv[2][0], pv[2][1]);
-        pa1.y = cvt_pk_rn(pv[2][2], pv[2][3]);
-        pa1.z = cvt_pk_rn(pv[3][0], pv[3][1]);
-        pa1.w = cvt_pk_rn(pv[3][2], pv[3][3]);
-        float al[GS];
-        bool moved = false;
-#pragma unroll
-        for (int g = 0; g < GS; ++g) {
-            al[g] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(alpha), g));
-            moved |= (al[g] != 1.0f);
-        }
-        if (moved) {
+            for (int g = 0; g < GS; ++g)
+                al[g] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(alpha), g));
             float f[4];
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
@@ -971,6 +954,27 @@ decode_stream_kernel(SplitParams p) {
 #pragma unroll
                 for (int i = 0; i < 4; ++i) acc_o[j][i] *= f[i];
         }
+        const float m_sub = (m_run == -INFINITY) ? 0.0f : m_run;
+        float pv[4][4];
+        float psum = 0.0f;
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float pr = __builtin_amdgcn_exp2f(fmaf(raw[k][i], p.scale_log2, -m_sub));
+                psum += pr;
+                pv[k][i] = (MASK && c0 + 16 * k + 4 * q4 + i >= end) ? 0.0f : pr;
+            }
+        l_run += psum;
+        uint4 pa0, pa1;
+        pa0.x = cvt_pk_rn(pv[0][0], pv[0][1]);
+        pa0.y = cvt_pk_rn(pv[0][2], pv[0][3]);
+        pa0.z = cvt_pk_rn(pv[1][0], pv[1][1]);
+        pa0.w = cvt_pk_rn(pv[1][2], pv[1][3]);
+        pa1.x = cvt_pk_rn(pv[2][0], pv[2][1]);
+        pa1.y = cvt_pk_rn(pv[2][2], pv[2][3]);
+        pa1.z = cvt_pk_rn(pv[3][0], pv[3][1]);
+        pa1.w = cvt_pk_rn(pv[3][2], pv[3][3]);
         if (MASK) {
             // A masked token's V is zeroed: its slot may hold garbage norms.
 #pragma unroll
