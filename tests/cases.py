@@ -25,8 +25,18 @@ class DecodeCase:
     expected: np.ndarray     # oracle output (B, H_q, 128) fp16
 
 
+def _ramp(k, k_ramp):
+    """K rows scaled by 1 + k_ramp * t / n along the key axis (axis 2): scores
+    that grow along the sequence, so a running max keeps moving."""
+    if not k_ramp:
+        return k
+    n = k.shape[2]
+    f = 1.0 + k_ramp * np.arange(n, dtype=np.float32) / max(1, n)
+    return (k.astype(np.float32) * f[None, None, :, None]).astype(np.float16)
+
+
 def make_decode_case(seed, seq_lens, *, H_kv=8, gs=4, block_size=16, cb=None, extra_blocks=3,
-                     scale=None, fill=0, cb_v=None):
+                     scale=None, fill=0, cb_v=None, k_ramp=0.0):
     """Encode seeded K/V per sequence with the checker, scatter into a paged
     cache through a permuted block table, and compute the checker's output."""
     seq_lens = np.asarray(seq_lens, dtype=np.int32)
@@ -39,7 +49,7 @@ def make_decode_case(seed, seq_lens, *, H_kv=8, gs=4, block_size=16, cb=None, ex
     nmax = max(1, int(seq_lens.max()))
     W = (nmax + block_size - 1) // block_size + extra_blocks
     bt = synth.permuted_block_table(seed, B, W)
-    k = synth.kv_with_outliers(seed, (B, H_kv, nmax, D))
+    k = _ramp(synth.kv_with_outliers(seed, (B, H_kv, nmax, D)), k_ramp)
     v = synth.normal_f16(seed + 1, (B, H_kv, nmax, D))
     q = synth.normal_f16(seed + 2, (B, H_q, D))
     kp, kn, _ = O.encode(k, cb)
@@ -78,7 +88,7 @@ class PrefillCase:
 
 
 def make_prefill_case(seed, seq_q, seq_k, *, H_kv=8, gs=4, block_size=16, scale=None, fill=0,
-                      cb_v=None):
+                      cb_v=None, k_ramp=0.0):
     """Seeded K/V for each sequence's seq_k keys (encoded by the checker into a
     paged cache), queries for its last seq_q positions, and the checker's
     causal prefill output."""
@@ -90,7 +100,7 @@ def make_prefill_case(seed, seq_q, seq_k, *, H_kv=8, gs=4, block_size=16, scale=
     nmax = max(1, int(seq_k.max()))
     W = (nmax + block_size - 1) // block_size + 1
     bt = synth.permuted_block_table(seed, B, W)
-    k = synth.kv_with_outliers(seed, (B, H_kv, nmax, D))
+    k = _ramp(synth.kv_with_outliers(seed, (B, H_kv, nmax, D)), k_ramp)
     v = synth.normal_f16(seed + 1, (B, H_kv, nmax, D))
     cbv = cb if cb_v is None else np.asarray(cb_v, dtype=np.float32)
     kp, kn, _ = O.encode(k, cb)

@@ -169,6 +169,22 @@ def test_decode_scale_and_slack_max_seq_len(gpu):
     check(out, case.expected)
 
 
+@pytest.mark.parametrize("scale", [None, 0.5], ids=["default_scale", "scale0.5"])
+def test_decode_rising_scores(gpu, scale):
+    """K rows growing 6x along the sequence: the running max keeps moving, so
+    the O rescale runs on many chunks (both split kernels)."""
+    from sub0_amd import _native
+    print(f"[decode] rising scores scale={scale}", flush=True)
+    case = make_decode_case(3100 + (scale is not None), [4000, 1500, 37], H_kv=8, gs=4,
+                            scale=scale, fill=0xFF, k_ramp=5.0)
+    check(run_gpu_decode(case, gpu, gs=4, scale=scale), case.expected)
+    _native.set_stream_kernel(False)
+    try:
+        check(run_gpu_decode(case, gpu, gs=4, scale=scale), case.expected)
+    finally:
+        _native.set_stream_kernel(True)
+
+
 def test_decode_empty_sequence_gives_zero(gpu):
     case = make_decode_case(78, [0, 200], H_kv=8, gs=4)
     out = run_gpu_decode(case, gpu, gs=4, max_seq_len=200)

@@ -76,6 +76,20 @@ def test_prefill_matches_checker(gpu, name, seq_q, seq_k, H_kv, gs, dense):
     check(out, case.expected)
 
 
+@pytest.mark.parametrize("mode", ["paged", "dense", "key_split"])
+def test_prefill_rising_scores(gpu, mode):
+    """K rows growing 11x along each sequence: the lazy running max moves
+    past its first tile (about twice per query row on average).  (At a
+    softmax scale several times the default, scores this large turn the
+    last-bit rounding of q_rot -- the Hadamard MFMA's order, as the
+    reference's own hadamard128 helper, not the checker's sequential fp32
+    sum -- into errors above 2e-3, as they would for the reference.)"""
+    print(f"[prefill] rising scores mode={mode}", flush=True)
+    case = make_prefill_case(4650, [700, 96, 16], [700, 1400, 3000], H_kv=8, gs=4, k_ramp=10.0)
+    check(run_prefill(case, gpu, dense=(mode == "dense"), split=(mode == "key_split")),
+          case.expected)
+
+
 @pytest.mark.parametrize("split", [False, True], ids=["unsplit", "key_split"])
 @pytest.mark.parametrize("copy", [False, True], ids=["different", "equal_copy"])
 def test_prefill_separate_codebooks(gpu, split, copy):
