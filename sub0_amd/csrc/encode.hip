@@ -204,7 +204,9 @@ paged_encode_kernel(EncodeParams p) {
     const int64_t t = t32;
 
     // ---- load the vector (all P lanes of the group read the same 256 B) ----
-    float x[kD];
+    // Kept as packed fp16 pairs; each x_k is widened to fp32 once, where the
+    // chains use it (xf below).
+    uint32_t xw[kD / 2];
     {
         const uint16_t *src = role == 0 ? p.k + t * p.k_stride + (int64_t)h * kD
                                         : p.v + t * p.v_stride + (int64_t)h * kD;
@@ -213,14 +215,20 @@ paged_encode_kernel(EncodeParams p) {
         for (int q = 0; q < kD / 8; ++q) {
             uint4 w = make_uint4(0, 0, 0, 0);
             if (valid) w = s4[q];
-            const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                x[8 * q + 2 * e] = h2f((uint16_t)(ws[e] & 0xFFFFu));
-                x[8 * q + 2 * e + 1] = h2f((uint16_t)(ws[e] >> 16));
-            }
+            xw[4 * q + 0] = w.x;
+            xw[4 * q + 1] = w.y;
+            xw[4 * q + 2] = w.z;
+            xw[4 * q + 3] = w.w;
         }
     }
+    // x_k in fp32 (exact).  The empty asm makes the widened value opaque, so
+    // the compiler cannot fold the conversion into every fma that uses it
+    // (v_fma_mix_f32, about twice the issue cost of v_fma_f32 on gfx950).
+    auto xf = [&](int k) CDA_INLINE -> float {
+        float v = h2f((uint16_t)((k & 1) ? (xw[k >> 1] >> 16) : (xw[k >> 1] & 0xFFFFu)));
+        asm volatile("" : "+v"(v));
+        return v;
+    };
 
     // ---- rotation: the fma chains as a tree ---------------------------------
     const float hval = __int_as_float(0x3db504f3);    // fp32(1/sqrt(128))
@@ -231,7 +239,7 @@ paged_encode_kernel(EncodeParams p) {
     {
         float c = 0.0f;
 #pragma unroll
-        for (int k = 0; k < P; ++k) c = fmaf(x[k], hs[k], c);
+        for (int k = 0; k < P; ++k) c = fmaf(xf(k), hs[k], c);
         ch[0] = c;
     }
 #pragma unroll
@@ -241,12 +249,14 @@ paged_encode_kernel(EncodeParams p) {
 #pragma unroll
         for (int m = 0; m < cnt; ++m) ch[m + cnt] = ch[m];
 #pragma unroll
-        for (int k = k0; k < 2 * k0; ++k)
+        for (int k = k0; k < 2 * k0; ++k) {
+            const float xk = xf(k);
 #pragma unroll
             for (int m = 0; m < 2 * cnt; ++m) {
                 const bool neg = (__builtin_popcount((unsigned)(k & (P * m))) & 1) != 0;
-                ch[m] = fmaf(x[k], neg ? -hs[k % P] : hs[k % P], ch[m]);
+                ch[m] = fmaf(xk, neg ? -hs[k % P] : hs[k % P], ch[m]);
             }
+        }
     }
 
     // ---- fp16 rounding, squares, norm (reference order) ---------------------
