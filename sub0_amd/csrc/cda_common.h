@@ -42,6 +42,15 @@ inline size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 #define CDA_INLINE __attribute__((always_inline))
 
 // fp16 bits -> fp32 (exact).
+// fp16(RN32(v)): the fp32 value is materialised first (an empty asm makes it
+// opaque), so the compiler cannot fuse the operation that produced it with
+// the conversion into one rounding (v_fma_mixlo_f16).  The reference rounds
+// twice: its fp32 arithmetic, then .to(torch.float16).
+__device__ __forceinline__ uint16_t f2h_after_f32(float v) {
+    asm volatile("" : "+v"(v));
+    return __half_as_ushort(__float2half_rn(v));
+}
+
 __device__ __forceinline__ float h2f(uint16_t h) {
     return __half2float(__ushort_as_half(h));
 }

@@ -1082,8 +1082,8 @@ rotate_q_kernel(const uint16_t *q, const float *R, uint16_t *q_rot, int H_q,
         a1 = fmaf(qs[hh][k], r.y, a1);
     }
     const int64_t row = ((int64_t)b * H_q + h0 + hh) * kD;
-    q_rot[row + j] = __half_as_ushort(__float2half_rn(a0));
-    q_rot[row + j + 1] = __half_as_ushort(__float2half_rn(a1));
+    q_rot[row + j] = f2h_after_f32(a0);
+    q_rot[row + j + 1] = f2h_after_f32(a1);
 }
 
 constexpr int kMaxSplits = 1024;
@@ -1205,10 +1205,10 @@ combine_kernel(const float *part_o, const float *part_ml, const float *R, uint16
         o.w = sum_halves(o.w);
         const float inv = 1.0f / fmaxf(L, 1e-30f);
         if (HPB == 4 && half == 0) {
-            orot[hh][d4 + 0] = h2f(__half_as_ushort(__float2half_rn(o.x * inv)));
-            orot[hh][d4 + 1] = h2f(__half_as_ushort(__float2half_rn(o.y * inv)));
-            orot[hh][d4 + 2] = h2f(__half_as_ushort(__float2half_rn(o.z * inv)));
-            orot[hh][d4 + 3] = h2f(__half_as_ushort(__float2half_rn(o.w * inv)));
+            orot[hh][d4 + 0] = h2f(f2h_after_f32(o.x * inv));
+            orot[hh][d4 + 1] = h2f(f2h_after_f32(o.y * inv));
+            orot[hh][d4 + 2] = h2f(f2h_after_f32(o.z * inv));
+            orot[hh][d4 + 3] = h2f(f2h_after_f32(o.w * inv));
         }
         if (HPB == 1 && half == 0)
             *reinterpret_cast<float4 *>(&orot[wsub][d4]) = make_float4(o.x, o.y, o.z, o.w);
@@ -1224,8 +1224,8 @@ combine_kernel(const float *part_o, const float *part_ml, const float *R, uint16
                          orot[3][lane + 64];
         // Every lane has read all four rows before row 0 is overwritten.
         __builtin_amdgcn_wave_barrier();
-        orot[0][lane] = h2f(__half_as_ushort(__float2half_rn(s0 * inv)));
-        orot[0][lane + 64] = h2f(__half_as_ushort(__float2half_rn(s1 * inv)));
+        orot[0][lane] = h2f(f2h_after_f32(s0 * inv));
+        orot[0][lane + 64] = h2f(f2h_after_f32(s1 * inv));
         __builtin_amdgcn_wave_barrier();
     }
     const float *r0 = Rs + lane * kRPad;
@@ -1246,8 +1246,8 @@ combine_kernel(const float *part_o, const float *part_ml, const float *R, uint16
         a1 = fmaf(o.w, y.w, a1);
     }
     const int64_t row = ((int64_t)b * H_q + h) * kD;
-    out[row + lane] = __half_as_ushort(__float2half_rn(a0));
-    out[row + lane + 64] = __half_as_ushort(__float2half_rn(a1));
+    out[row + lane] = f2h_after_f32(a0);
+    out[row + lane + 64] = f2h_after_f32(a1);
 }
 
 struct WsLayout {

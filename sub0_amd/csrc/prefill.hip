@@ -873,8 +873,8 @@ prefill_combine_kernel(const float *__restrict__ part_o, const float *__restrict
     // on index bit 0 runs in registers, bits 1-6 pair lane l with lane
     // l ^ 2^(b-1) (x_i + x_partner where bit b of i is clear, x_partner - x_i
     // where it is set): the Sylvester sum sum_k (-1)^popcount(j & k) x_k.
-    float x0 = (float)(_Float16)(o0 * inv_l);
-    float x1 = (float)(_Float16)(o1 * inv_l);
+    float x0 = h2f(f2h_after_f32(o0 * inv_l));
+    float x1 = h2f(f2h_after_f32(o1 * inv_l));
     {
         const float a = x0 + x1, b = x0 - x1;
         x0 = a;
@@ -888,9 +888,8 @@ prefill_combine_kernel(const float *__restrict__ part_o, const float *__restrict
         x1 = fmaf(sgn, x1, p1);
     }
     const float hs = 0.08838834764831845f;
-    typedef _Float16 half2_ __attribute__((ext_vector_type(2)));
-    const half2_ hv = {(_Float16)(x0 * hs), (_Float16)(x1 * hs)};
-    *reinterpret_cast<half2_ *>(out + row * kD + 2 * lane) = hv;
+    const uint32_t hv = (uint32_t)f2h_after_f32(x0 * hs) | ((uint32_t)f2h_after_f32(x1 * hs) << 16);
+    *reinterpret_cast<uint32_t *>(out + row * kD + 2 * lane) = hv;
 }
 
 // The attention kernel alone; with `partials` it writes split partials
@@ -1171,8 +1170,8 @@ dequant_rows_kernel(const uint8_t *codes, const float *norms, int64_t rows, int 
         }
 #pragma unroll
         for (int j = 0; j < 8; ++j)
-            w[j] = (uint32_t)__half_as_ushort(__float2half_rn(x[2 * j] * nrm)) |
-                   ((uint32_t)__half_as_ushort(__float2half_rn(x[2 * j + 1] * nrm)) << 16);
+            w[j] = (uint32_t)f2h_after_f32(x[2 * j] * nrm) |
+                   ((uint32_t)f2h_after_f32(x[2 * j + 1] * nrm) << 16);
     }
     uint4 *dst = reinterpret_cast<uint4 *>(out + (r * H + h) * kD + 16 * c);
     dst[0] = make_uint4(w[0], w[1], w[2], w[3]);
