@@ -48,6 +48,14 @@ def hadamard_matrix(d: int, *, dtype: torch.dtype = torch.float32,
     return (sign * h).to(dtype=dtype, device=device).contiguous()
 
 
+def half_rotate_pair(d: int, *, dtype: torch.dtype = torch.float32,
+                     device: torch.device | str | None = None) -> Tensor:
+    """The rotation applied once to Q, K and V and, inverted, to the output
+    (compression.py:60-67): the orthonormal Sylvester Hadamard is its own
+    inverse, so one matrix serves both directions."""
+    return hadamard_matrix(d, dtype=dtype, device=device)
+
+
 def uniform_centroids(num_levels: int, *, dtype: torch.dtype = torch.float32,
                       device: torch.device | str | None = None) -> Tensor:
     """Bin midpoints of ``num_levels`` equal bins over [-1, 1]."""

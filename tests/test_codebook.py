@@ -12,6 +12,7 @@ def test_lloyd_beta_codebooks_bit_exact(codebooks):
 
 def test_hadamard_and_uniform_bit_exact(codebooks):
     assert np.array_equal(C.hadamard_matrix(128).numpy(), codebooks["hadamard128"])
+    assert np.array_equal(C.half_rotate_pair(128).numpy(), codebooks["hadamard128"])
     for L in (16, 4):
         assert np.array_equal(C.uniform_centroids(L).numpy(), codebooks[f"uniform{L}"])
 
