@@ -124,3 +124,39 @@ def test_fa2_fork_build_stub():
     from sub0_amd.cda.kernels_vllm_fa2_fork import build
     build.load()
     assert hasattr(torch.ops._cda_vllm_fa2_fork_C, "varlen_fwd")
+
+
+def test_fa2_fork_interface_rejects_unsupported():
+    """The argument checks of kernels_vllm_fa2_fork's Python entry points
+    (reference interface.py:200-217, 367-372) and this build's explicit
+    limits; all raise before any kernel is reached."""
+    from sub0_amd.cda import kernels_vllm_fa2_fork as F
+    q = torch.zeros(4, 8, 128, dtype=torch.float16)
+    k = torch.zeros(4, 2, 128, dtype=torch.float16)
+    cu = torch.tensor([0, 4], dtype=torch.int32)
+    with pytest.raises(ValueError, match="must be provided"):
+        F.flash_attn_varlen_func(q, k, k, 4, cu, 4)
+    with pytest.raises(ValueError, match="cannot both"):
+        F.flash_attn_varlen_func(q, k, k, 4, cu, 4, cu_seqlens_k=cu, seqused_k=cu[1:])
+    with pytest.raises(ValueError, match="block_table"):
+        F.flash_attn_varlen_func(q, k, k, 4, cu, 4, cu_seqlens_k=cu, block_table=cu)
+    with pytest.raises(ValueError, match="fa_version"):
+        F.flash_attn_varlen_func(q, k, k, 4, cu, 4, cu_seqlens_k=cu, fa_version=3)
+    with pytest.raises(NotImplementedError, match="dropout"):
+        F.flash_attn_varlen_func(q, k, k, 4, cu, 4, cu_seqlens_k=cu, dropout_p=0.1)
+    with pytest.raises(NotImplementedError, match="LSE"):
+        F.flash_attn_varlen_func(q, k, k, 4, cu, 4, cu_seqlens_k=cu, return_softmax_lse=True)
+    with pytest.raises(ValueError, match="exactly two"):
+        F.flash_attn_varlen_func(q, k, k, 4, cu, 4, cu_seqlens_k=cu, window_size=(1,))
+    ki = torch.zeros(4, 2, 64, dtype=torch.uint8)
+    kn = torch.zeros(4, 2)
+    cb = torch.zeros(16)
+    with pytest.raises(ValueError, match="must be provided"):
+        F.flash_attn_varlen_compressed_kv_fused_func(q, ki, kn, ki, kn, cb, cb, 4, cu, 4)
+    with pytest.raises(ValueError, match="seqused_k"):
+        F.flash_attn_varlen_compressed_kv_fused_func(q, ki, kn, ki, kn, cb, cb, 4, cu, 4,
+                                                     block_table=cu)
+    with pytest.raises(ValueError, match="3D or 4D"):
+        F.dequantize_compressed_kv(ki[0], kn[0], ki[0], kn[0], cb, cb)
+    with pytest.raises(ImportError):
+        F.register_vllm_backend()

@@ -139,3 +139,55 @@ def test_fork_varlen_compressed(gpu, codebooks, causal, paged):
     assert r[0] is out
     err = float((out.float() - ref.float()).abs().max())
     assert err <= TOL, err
+
+
+@pytest.mark.parametrize("entry", ["dense", "two_step_4d", "fused_paged"])
+def test_fork_python_interface(gpu, codebooks, entry):
+    """The Python entry points of kernels_vllm_fa2_fork (interface.py of the
+    reference): dense varlen, the two-step bridge on the compressor's
+    (B, H_kv, N, 64) layout, and the fused call on paged pools."""
+    from sub0_amd.cda import kernels_vllm_fa2_fork as F
+    cb = codebooks["lloyd_beta16"]
+    H_kv, H_q = 8, 32
+    lens = [256, 256] if entry == "two_step_4d" else [300, 97, 1000]
+    qlens = [16, 64] if entry == "two_step_4d" else [37, 1, 64]
+    kp, kn, vp, vn = _rows(8400, lens, H_kv, cb)
+    q = _t(synth.normal_f16(8403, (sum(qlens), H_q, 128)), gpu)
+    cu_q = torch.tensor(np.concatenate([[0], np.cumsum(qlens)]), dtype=torch.int32, device=gpu)
+    cu_k = torch.tensor(np.concatenate([[0], np.cumsum(lens)]), dtype=torch.int32, device=gpu)
+    kd = _t(O.decode_rotated(kp, kn, cb), gpu)
+    vd = _t(O.decode_rotated(vp, vn, cb), gpu)
+    ref = _attn_ref(q, kd, vd, cu_q.tolist(), lens, float(1 / np.sqrt(128)), True)
+    cbt = _t(cb, gpu)
+    print(f"[torch-ops] fork python interface {entry}", flush=True)
+    if entry == "dense":
+        out = F.flash_attn_varlen_func(q, kd, vd, max(qlens), cu_q, max(lens),
+                                       cu_seqlens_k=cu_k, causal=True)
+    elif entry == "two_step_4d":
+        B, N = len(lens), lens[0]
+
+        def slot(a):                      # (B*N, H_kv, .) -> (B, H_kv, N, .)
+            return _t(a.reshape((B, N) + a.shape[1:]).swapaxes(1, 2), gpu)
+        out = F.flash_attn_varlen_compressed_kv_func(
+            q, slot(kp), slot(kn), slot(vp), slot(vn), cbt, cbt, max(qlens), cu_q, N, cu_k,
+            causal=True)
+    else:
+        bs, W = 16, (max(lens) + 15) // 16
+        bt = synth.permuted_block_table(8404, len(lens), W)
+        nb = len(lens) * W
+        pools = [np.zeros((nb * bs,) + a.shape[1:], a.dtype) for a in (kp, kn, vp, vn)]
+        k0 = 0
+        for b, L in enumerate(lens):
+            t = np.arange(L)
+            slots = bt[b][t // bs] * bs + t % bs
+            for pool, a in zip(pools, (kp, kn, vp, vn)):
+                pool[slots] = a[k0:k0 + L]
+            k0 += L
+        kpp, knp, vpp, vnp = (_t(p.reshape((nb, bs) + p.shape[1:]), gpu) for p in pools)
+        out = F.flash_attn_varlen_compressed_kv_fused_func(
+            q, kpp, knp, vpp, vnp, cbt, cbt, max(qlens), cu_q, max(lens),
+            seqused_k=torch.tensor(lens, dtype=torch.int32, device=gpu), block_table=_t(bt, gpu),
+            causal=True)
+    torch.cuda.synchronize()
+    err = float((out.float() - ref.float()).abs().max())
+    assert err <= TOL, err
