@@ -1053,6 +1053,8 @@ def main(argv=None):
                          "the general split kernel)")
     ap.add_argument("--k2v2", action="store_true",
                     help="decode over a K2V2 cache (4-level codebook, 80-byte slots) instead of K4V4")
+    ap.add_argument("--three-launch", action="store_true",
+                    help="rotate / split / combine launches instead of the single-launch decode")
     ap.add_argument("--general-kernel", action="store_true",
                     help="forbid the page-streaming split kernel (A/B diagnostic)")
     ap.add_argument("--identity-block-table", action="store_true",
@@ -1092,6 +1094,8 @@ def main(argv=None):
         return table2_main(args)
     if args.general_kernel:
         _native.set_stream_kernel(False)
+    if args.three_launch:
+        _native.set_fused_kernel(False)
     B, N = args.B, args.N
 
     global H_Q
@@ -1162,6 +1166,8 @@ def main(argv=None):
     # Both code widths (8 KV heads, one codebook) take the page-streaming kernel
     # unless it is switched off.
     kernel = "decode_split_kernel" if args.general_kernel else "decode_stream_kernel"
+    if kernel == "decode_stream_kernel" and not args.three_launch and args.tile_n == 0:
+        kernel = "decode_stream_kernel<FUSED>"    # the single-launch form
     variant = "K4V4" if levels == 16 else "K2V2"
     if args.k4v2:
         variant = "K4V2 (104-byte slots)"

@@ -155,6 +155,18 @@ int cda_decode_set_timing_events(void *start_event, void *stop_event);
  * has one decode kernel; this exists for A/B measurement and tests. */
 int cda_decode_set_stream_kernel(int enable);
 
+/* Selects the single-launch decode for later calls (process-wide; default 1).
+ * enable=1 lets cda_decode_full_hmma_v3 run, where the page-streaming kernel
+ * applies with one codebook pointer for K and V and the library's split plan
+ * (tile_n = 0, or the tile_n that cda_decode_plan returns for tile_n = 0, which
+ * is what the reference-shaped wrapper passes), one kernel per call: each workgroup takes one KV head over a token
+ * range, rotates q itself, merges its waves' partials and, when its range is
+ * the whole sequence, writes out (otherwise combine_kernel follows).  The
+ * timing events above then bracket that kernel.  enable=0 keeps the
+ * rotate / split / combine launches.  No reference counterpart: for A/B
+ * measurement and tests. */
+int cda_decode_set_fused_kernel(int enable);
+
 /* ---------------------------------------------------------------- encode --
  * Replaces the reference pybind function
  *   cda_paged_encode_fused(K, V, slot_mapping, flat_cache, cb_K, cb_V)

@@ -28,6 +28,7 @@ SYMBOLS = (
     "cda_decode_full_hmma_v3",
     "cda_decode_set_timing_events",
     "cda_decode_set_stream_kernel",
+    "cda_decode_set_fused_kernel",
     "cda_decode_full_hmma_v3_k4v2",
     "cda_paged_encode_fused_k4v2",
     "cda_fa2_paged_cache_to_dense_rotated_k4v2",
@@ -103,6 +104,8 @@ def lib():
         L.cda_decode_set_timing_events.argtypes = [_P, _P]
         L.cda_decode_set_stream_kernel.restype = _I32
         L.cda_decode_set_stream_kernel.argtypes = [_I32]
+        L.cda_decode_set_fused_kernel.restype = _I32
+        L.cda_decode_set_fused_kernel.argtypes = [_I32]
         L.cda_decode_full_hmma_v3_k4v2.restype = _I32
         L.cda_decode_full_hmma_v3_k4v2.argtypes = [
             _P, _P, _I64, _I32, _I32, _P, _I32, _P, _P, _P, _P, _P, _P,
@@ -314,6 +317,12 @@ def set_stream_kernel(enable: bool) -> None:
     """Allow (default) or forbid the page-streaming decode kernel for later
     calls in this process; forbidding it always runs the general kernel."""
     _check(lib().cda_decode_set_stream_kernel(int(bool(enable))), "cda_decode_set_stream_kernel")
+
+
+def set_fused_kernel(enable: bool) -> None:
+    """Allow (default) or forbid the single-launch decode for later calls in
+    this process; forbidding it keeps the rotate / split / combine launches."""
+    _check(lib().cda_decode_set_fused_kernel(int(bool(enable))), "cda_decode_set_fused_kernel")
 
 
 def decode_algorithmic_bytes(B: int, N: int, H_q: int = 32, H_kv: int = 8,

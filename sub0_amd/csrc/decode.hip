@@ -75,6 +75,15 @@ struct SplitParams {
     // Score-domain QK (decode_stream_kernel's SQK form): 1 if cb_k holds the
     // 16-level uniform codebook (2i + 1)/16 - 1, written by rotate_q_kernel.
     const int *k_uniform;
+    // Single-launch form (decode_stream_kernel's FUSED form): one workgroup
+    // per (sequence, split, KV head), its waves on consecutive token ranges
+    // of wave_tokens each; the workgroup rotates q itself and, when the split
+    // covers the whole sequence (n_splits == 1), writes out itself.
+    const uint16_t *q;          // (B, H_q, 128) fp16, un-rotated
+    const float *R;             // (128, 128) fp32 rotation
+    uint16_t *out;              // (B, H_q, 128) fp16
+    int wave_tokens;            // multiple of 64
+    int xcd_map;                // 1: the 8 heads of a (sequence, split) share an XCD
 };
 
 __device__ __forceinline__ floatx4 mfma16(uint4 a, uint4 b, floatx4 c) {
@@ -541,6 +550,13 @@ constexpr int kStreamPages = 4;
 constexpr int kStreamRingOff = kLut2Bytes;
 constexpr int kStreamPidOff = kStreamRingOff + kWaves * kStreamPages * kHeadPage;
 constexpr int kStreamLds = kStreamPidOff + kStreamMaxPages * 4;           // 143360 B
+// FUSED form: a workgroup covers up to 4096 pages of one head, and stages q
+// (fp32) and q_rot (fp16) of its GQA group after the page rows.
+constexpr int kFusedMaxPages = 4096;
+constexpr int kFusedQOff = kStreamPidOff + kFusedMaxPages * 4;
+constexpr int kFusedQrOff = kFusedQOff + 8 * kD * 4;
+constexpr int kFusedLds = kFusedQrOff + 8 * kD * 2;                         // 159744 B
+static_assert(kFusedLds <= 160 * 1024, "FUSED LDS");
 
 // K2V2 V slot of token t: the four tokens read together (4*q4 + i, q4 =
 // 0..3) land in four consecutive 32-byte slots (an involution).
@@ -557,13 +573,14 @@ __device__ __forceinline__ uint32_t bfi(uint32_t m, uint32_t a, uint32_t b) {
 // code (the subnormal code * 2^-24, exact; no table, no multiply), so
 // q_rot . code = acc * 2^24 exactly up to fp32 accumulation; V is decoded
 // as in the default form, through a table of cb_v.
-template <int GS, int L, bool SQK = false>
+template <int GS, int L, bool SQK = false, bool FUSED = false>
 __global__ void __launch_bounds__(kThreads, 1)
 decode_stream_kernel(SplitParams p) {
-    if (!SQK && p.cb_same && !*p.cb_same) return;   // different codebooks: the general kernel runs
+    if (!FUSED && !SQK && p.cb_same && !*p.cb_same) return;   // different codebooks: the general kernel runs
     static_assert(L == 16 || L == 4, "4-bit or 2-bit codes");
     static_assert(!SQK || L == 16, "score-domain QK: 4-bit K codes");
-    __shared__ __align__(16) uint8_t smem[kStreamLds];
+    static_assert(!(SQK && FUSED), "the score-domain form runs as three launches");
+    __shared__ __align__(16) uint8_t smem[FUSED ? kFusedLds : kStreamLds];
     constexpr int S = (L == 16) ? 144 : 80;        // slot bytes
     constexpr int KB = (L == 16) ? 64 : 32;        // code bytes per role
     constexpr int kRow = 8 * S;                    // one token row, all heads
@@ -573,20 +590,43 @@ decode_stream_kernel(SplitParams p) {
     constexpr uint32_t kNo = 32 * KB;              // norms within a ring page
     static_assert(kWaves * kStreamPages * kHP + kStreamRingOff <= kStreamPidOff, "ring fits");
 
-    const int sp = blockIdx.x;
-    const int b = blockIdx.z;
     const int tid = threadIdx.x;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int lane = tid & 63;
-    const int h = wave;
     const int r16 = lane & 15;
     const int q4 = lane >> 4;
+    int sp, b, h;
+    if constexpr (FUSED) {
+        // Linear id -> (unit = (sequence, split), head).  The hardware deals
+        // workgroups to the 8 XCDs round-robin by linear id; with xcd_map the
+        // 8 heads of a unit go to one XCD, so the 64-byte segments that
+        // neighbouring heads' slots share are fetched into one L2.
+        const int pl = blockIdx.x;
+        int u;
+        if (p.xcd_map) {
+            const int i = pl >> 3;
+            h = i & 7;
+            u = ((i >> 3) << 3) + (pl & 7);
+        } else {
+            h = pl & 7;
+            u = pl >> 3;
+        }
+        sp = u % p.n_splits;
+        b = u / p.n_splits;
+    } else {
+        sp = blockIdx.x;
+        b = blockIdx.z;
+        h = wave;
+    }
 
     const int seq_len =
         __builtin_amdgcn_readfirstlane(min(p.seq_lens[b], p.bt_stride * p.block_size));
     const int start = sp * p.tile_n;
     const int end = min(start + p.tile_n, seq_len);
     const int64_t part_row = ((int64_t)b * p.n_splits + sp) * p.H_q + (int64_t)h * GS;
+    // This wave's token range: the whole split, or (FUSED) its own share.
+    const int wstart = FUSED ? min(start + wave * p.wave_tokens, end) : start;
+    const int wend = FUSED ? min(wstart + p.wave_tokens, end) : end;
     if (SQK && !*p.k_uniform) {
         // Not the uniform codebook: the output is NaN rather than wrong.
         if (q4 == 0 && r16 < GS) {
@@ -596,7 +636,14 @@ decode_stream_kernel(SplitParams p) {
         for (int i = lane; i < GS * kD; i += 64) p.part_o[part_row * kD + i] = __builtin_nanf("");
         return;
     }
+    if (FUSED && start >= end && p.n_splits == 1) {
+        // Empty sequence: the merge of no keys is 0 (weights 0, l clamped).
+        for (int i = tid; i < GS * kD; i += kThreads)
+            p.out[((int64_t)b * p.H_q + (int64_t)h * GS) * kD + i] = 0;
+        return;
+    }
     if (start >= end) {
+        if (FUSED && wave != 0) return;
         if (q4 == 0 && r16 < GS) {
             p.part_ml[(part_row + r16) * 2 + 0] = -INFINITY;
             p.part_ml[(part_row + r16) * 2 + 1] = 0.0f;
@@ -621,7 +668,9 @@ decode_stream_kernel(SplitParams p) {
     }
 
     const int bs = p.block_size;
-    const int npages = (end - start + 15) >> 4;
+    const int npages = (end - start + 15) >> 4;          // the workgroup's pages
+    const int wpage0 = (wstart - start) >> 4;            // this wave's first among them
+    const int wnpages = (wend - wstart + 15) >> 4;
     const uint32_t ring_w = __builtin_amdgcn_readfirstlane(lds_u32addr(smem)) + kStreamRingOff +
                             wave * (kStreamPages * kHP);
     int32_t *page_row = reinterpret_cast<int32_t *>(smem + kStreamPidOff);
@@ -646,7 +695,7 @@ decode_stream_kernel(SplitParams p) {
     };
     // DMA of page t (row from the workgroup's table) into ring slot k.
     auto issue = [&](int t, int k) CDA_INLINE {
-        issue_row(__builtin_amdgcn_readfirstlane(page_row[t]), k);
+        issue_row(__builtin_amdgcn_readfirstlane(page_row[wpage0 + t]), k);
     };
     // The first chunk's pages straight from the block table (wave-uniform
     // loads), before the tables are built: their latency overlaps the set-up.
@@ -654,13 +703,18 @@ decode_stream_kernel(SplitParams p) {
         const int32_t *bt = p.block_table + (int64_t)b * p.bt_stride;
 #pragma unroll
         for (int k = 0; k < kStreamPages; ++k)
-            if (k < npages) {
-                const int t0 = start + 16 * k;
+            if (k < wnpages) {
+                const int t0 = wstart + 16 * k;
                 issue_row((int64_t)__builtin_amdgcn_readfirstlane(bt[t0 / bs]) * bs + t0 % bs, k);
             }
     }
     uint4 qb[4];
-    {
+    if constexpr (FUSED) {
+        // q of this head's GQA group as fp32, for the rotation below.
+        float *qs = reinterpret_cast<float *>(smem + kFusedQOff);
+        const uint16_t *qg = p.q + ((int64_t)b * p.H_q + (int64_t)h * GS) * kD;
+        for (int i = tid; i < GS * kD; i += kThreads) qs[i] = h2f(qg[i]);
+    } else {
         const uint16_t *qg =
             p.q_rot + ((int64_t)b * p.H_q + (int64_t)h * GS + (r16 & (GS - 1))) * kD + 32 * q4;
 #pragma unroll
@@ -696,7 +750,27 @@ decode_stream_kernel(SplitParams p) {
                 lut[i] = __float_as_uint(cbs[(i & 1) ? ((e >> 4) & 3) : (e >> 6)]);
         }
     }
+    if constexpr (FUSED) {
+        // q_rot = fp16(q @ R): the fp32 fma chain over k in ascending order,
+        // as rotate_q_kernel computes it (compression.py:290-291).
+        const float *qs = reinterpret_cast<const float *>(smem + kFusedQOff);
+        uint16_t *qr = reinterpret_cast<uint16_t *>(smem + kFusedQrOff);
+        for (int o = tid; o < GS * kD; o += kThreads) {
+            const float *qrow = qs + (o >> 7) * kD;
+            const float *rc = p.R + (o & (kD - 1));
+            float a = 0.0f;
+#pragma unroll 16
+            for (int k = 0; k < kD; ++k) a = fmaf(qrow[k], rc[k * kD], a);
+            qr[o] = f2h_after_f32(a);
+        }
+    }
     __syncthreads();
+    if constexpr (FUSED) {
+        const uint16_t *qr = reinterpret_cast<const uint16_t *>(smem + kFusedQrOff) +
+                             (r16 & (GS - 1)) * kD + 32 * q4;
+#pragma unroll
+        for (int s = 0; s < 4; ++s) qb[s] = *reinterpret_cast<const uint4 *>(qr + 8 * s);
+    }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
     const uint32_t rb0 = (uint32_t)(kStreamRingOff + wave * (kStreamPages * kHP));
@@ -887,21 +961,21 @@ decode_stream_kernel(SplitParams p) {
     // ---- one chunk of four pages starting at page 4c (token c0).
     auto step = [&](int c, auto masked) CDA_INLINE {
         constexpr bool MASK = decltype(masked)::value;
-        const int c0 = start + 64 * c;
+        const int c0 = wstart + 64 * c;
         const int p0 = 4 * c;
         __builtin_amdgcn_s_waitcnt(0x0F70);        // this chunk's DMAs (the only ones in flight)
         asm volatile("" ::: "memory");
         PageRegs r[4];
         read_page(r[0], IC<0>{});
-        if (!MASK || p0 + 1 < npages) read_page(r[1], IC<1>{});
-        if (!MASK || p0 + 2 < npages) read_page(r[2], IC<2>{});
-        if (!MASK || p0 + 3 < npages) read_page(r[3], IC<3>{});
+        if (!MASK || p0 + 1 < wnpages) read_page(r[1], IC<1>{});
+        if (!MASK || p0 + 2 < wnpages) read_page(r[2], IC<2>{});
+        if (!MASK || p0 + 3 < wnpages) read_page(r[3], IC<3>{});
         if (MASK) {
             // Pages past the split are not read: zero codes and norms (their
             // tokens are masked out below).
 #pragma unroll
             for (int k = 1; k < 4; ++k)
-                if (p0 + k >= npages) {
+                if (p0 + k >= wnpages) {
                     r[k].kq = make_uint4(0, 0, 0, 0);
                     r[k].nk = 0.0f;
 #pragma unroll
@@ -918,7 +992,7 @@ decode_stream_kernel(SplitParams p) {
             const int n0 = p0 + 4;
 #pragma unroll
             for (int k = 0; k < 4; ++k)
-                if (n0 + k < npages) issue(n0 + k, k);
+                if (n0 + k < wnpages) issue(n0 + k, k);
         }
         floatx4 sc[4];
         if constexpr (SQK) {
@@ -941,7 +1015,7 @@ decode_stream_kernel(SplitParams p) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 raw[k][i] = sc[k][i];
-                if (MASK && c0 + 16 * k + 4 * q4 + i >= end) raw[k][i] = -INFINITY;
+                if (MASK && c0 + 16 * k + 4 * q4 + i >= wend) raw[k][i] = -INFINITY;
             }
         float cmax = max3f(max3f(raw[0][0], raw[0][1], raw[0][2]),
                            max3f(raw[0][3], raw[1][0], raw[1][1]),
@@ -985,7 +1059,7 @@ decode_stream_kernel(SplitParams p) {
             for (int i = 0; i < 4; ++i) {
                 const float pr = __builtin_amdgcn_exp2f(fmaf(raw[k][i], p.scale_log2, -m_sub));
                 psum += pr;
-                pv[k][i] = (MASK && c0 + 16 * k + 4 * q4 + i >= end) ? 0.0f : pr;
+                pv[k][i] = (MASK && c0 + 16 * k + 4 * q4 + i >= wend) ? 0.0f : pr;
             }
         l_run += psum;
         uint4 pa0, pa1;
@@ -1003,15 +1077,15 @@ decode_stream_kernel(SplitParams p) {
             for (int k = 0; k < 4; ++k)
 #pragma unroll
                 for (int i = 0; i < 4; ++i)
-                    if (c0 + 16 * k + 4 * q4 + i >= end) r[k].nv[i] = 0.0f;
+                    if (c0 + 16 * k + 4 * q4 + i >= wend) r[k].nv[i] = 0.0f;
         }
         pv_pair(pa0, r[0], r[1]);
         pv_pair(pa1, r[2], r[3]);
     };
 #undef CDA_PAIR
 
-    const int nchunks = (npages + 3) >> 2;
-    const int nfull = (end - start) >> 6;
+    const int nchunks = (wnpages + 3) >> 2;
+    const int nfull = (wend - wstart) >> 6;
     for (int c = 0; c < nfull; ++c) {
         step(c, std::false_type{});
         if constexpr (SQK) {
@@ -1021,6 +1095,83 @@ decode_stream_kernel(SplitParams p) {
     if (nfull < nchunks) step(nfull, std::true_type{});
 
     const float l = rows_sum(l_run);
+    if constexpr (FUSED) {
+        // Merge the eight waves' partials of this head's GQA group
+        // (attention.py:239-272, log2 domain).  Each wave parks its (O, m, l)
+        // in its own ring area, idle once its last chunk is read.
+        auto wave_part = [&](int w) CDA_INLINE {
+            return reinterpret_cast<float *>(smem + kStreamRingOff + w * (kStreamPages * kHP));
+        };
+        float *mine = wave_part(wave);
+        if (q4 == 0 && r16 < GS) {
+            mine[GS * kD + r16] = m_run;
+            mine[GS * kD + GS + r16] = l;
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int g = 4 * q4 + i;
+            if (g < GS) {
+                float4 *dst = reinterpret_cast<float4 *>(mine + g * kD + 8 * r16);
+                dst[0] = make_float4(acc_o[0][i], acc_o[1][i], acc_o[2][i], acc_o[3][i]);
+                dst[1] = make_float4(acc_o[4][i], acc_o[5][i], acc_o[6][i], acc_o[7][i]);
+            }
+        }
+        __syncthreads();
+        float *orot = reinterpret_cast<float *>(smem);   // the table area, free now
+        for (int o = tid; o < GS * kD; o += kThreads) {
+            const int g = o >> 7, d = o & (kD - 1);
+            float mw[kWaves];
+            float M = -INFINITY;
+#pragma unroll
+            for (int w = 0; w < kWaves; ++w) {
+                mw[w] = wave_part(w)[GS * kD + g];
+                M = fmaxf(M, mw[w]);
+            }
+            float Ls = 0.0f, Os = 0.0f;
+#pragma unroll
+            for (int w = 0; w < kWaves; ++w) {
+                const float a = (mw[w] == -INFINITY) ? 0.0f : exp2f(mw[w] - M);
+                Ls = fmaf(a, wave_part(w)[GS * kD + GS + g], Ls);
+                Os = fmaf(a, wave_part(w)[g * kD + d], Os);
+            }
+            if (p.n_splits == 1) {
+                // As the merge's epilogue: fp16(O / l) (attention.py:93).
+                orot[o] = h2f(f2h_after_f32(Os * (1.0f / fmaxf(Ls, 1e-30f))));
+            } else {
+                p.part_o[(part_row + g) * kD + d] = Os;
+                if (d == 0) {
+                    p.part_ml[(part_row + g) * 2 + 0] = M;
+                    p.part_ml[(part_row + g) * 2 + 1] = Ls;
+                }
+            }
+        }
+        if (p.n_splits != 1) return;                     // combine_kernel merges the splits
+        __syncthreads();
+        // out[j] = sum_k fp16(O_rot)[k] * R[j][k], k ascending (compression.py:293-296):
+        // thread j reads row j of R once for the group's GS heads.
+        if (tid < kD) {
+            const float4 *rrow = reinterpret_cast<const float4 *>(p.R + tid * kD);
+            float a[GS];
+#pragma unroll
+            for (int g = 0; g < GS; ++g) a[g] = 0.0f;
+#pragma unroll 8
+            for (int k4 = 0; k4 < kD / 4; ++k4) {
+                const float4 x = rrow[k4];
+#pragma unroll
+                for (int g = 0; g < GS; ++g) {
+                    const float4 o4 = *reinterpret_cast<const float4 *>(orot + g * kD + 4 * k4);
+                    a[g] = fmaf(o4.x, x.x, a[g]);
+                    a[g] = fmaf(o4.y, x.y, a[g]);
+                    a[g] = fmaf(o4.z, x.z, a[g]);
+                    a[g] = fmaf(o4.w, x.w, a[g]);
+                }
+            }
+            const int64_t orow = (int64_t)b * p.H_q + (int64_t)h * GS;
+#pragma unroll
+            for (int g = 0; g < GS; ++g) p.out[(orow + g) * kD + tid] = f2h_after_f32(a[g]);
+        }
+        return;
+    }
     if (q4 == 0 && r16 < GS) {
         p.part_ml[(part_row + r16) * 2 + 0] = m_run;
         p.part_ml[(part_row + r16) * 2 + 1] = l;
@@ -1254,6 +1405,13 @@ struct WsLayout {
     size_t q_rot, part_o, part_ml, flag, total;
 };
 
+// Plan of the single-launch form: workgroups of one KV head over
+// 8 * wave_tokens tokens (each wave at least one 64-token chunk), about one
+// workgroup per CU over all sequences and heads, at most 4096 pages (64K
+// tokens) per workgroup.  Never more splits than cda_decode_plan's, so its
+// partials fit the same workspace.
+void fused_plan(int B, int H_kv, int max_seq_len, int *wave_tokens, int *n_splits);
+
 WsLayout ws_layout(int B, int H_q, int n_splits) {
     WsLayout w;
     size_t off = 0;
@@ -1274,6 +1432,9 @@ thread_local hipEvent_t g_split_start = nullptr;
 thread_local hipEvent_t g_split_stop = nullptr;
 // Lets tests run the general kernel on shapes the streaming kernel also covers.
 bool g_allow_stream = true;
+// Lets tests and benchmarks run the three-launch form where the single-launch
+// form also applies.
+bool g_allow_fused = true;
 
 int num_cus() {
     static int cached = 0;
@@ -1287,6 +1448,21 @@ int num_cus() {
             cached = 256;
     }
     return cached;
+}
+
+void fused_plan(int B, int H_kv, int max_seq_len, int *wave_tokens, int *n_splits) {
+    const int n = max_seq_len > 0 ? max_seq_len : 1;
+    const int units = B * H_kv;
+    int s = (num_cus() + units - 1) / units;
+    const int max_by_len = (n + 8 * kStreamPages * 16 - 1) / (8 * kStreamPages * 16);
+    if (s > max_by_len) s = max_by_len;
+    const int min_by_len = (n + 16 * kFusedMaxPages - 1) / (16 * kFusedMaxPages);
+    if (s < min_by_len) s = min_by_len;
+    if (s < 1) s = 1;
+    int wg = (n + s - 1) / s;
+    wg = (wg + 511) / 512 * 512;
+    *wave_tokens = wg / kWaves;
+    *n_splits = (n + wg - 1) / wg;
 }
 
 }  // namespace
@@ -1393,6 +1569,72 @@ int decode_impl(const void *q, const void *kv_cache, int slot_bytes, int H_kv,
         CDA_REQUIRE(stream_shape && levels_k == 16,
                     f + ": the score-domain QK runs on the page-streaming kernel: K4V4 "
                         "144-byte slots, 8 KV heads, splits of at most 16384 tokens");
+    // Single launch: one workgroup per (sequence, split, KV head) rotates q,
+    // streams, merges its waves and (one split per sequence) writes out; more
+    // splits add the combine launch.  Taken with one codebook pointer and the
+    // library's split plan (tile_n 0, or the plan's own tile_n, which the
+    // reference-shaped wrapper passes).
+    int plan_tn = 0;
+    cda_decode_plan(B, H_q, H_kv, max_seq_len, 0, &plan_tn, nullptr);
+    if (stream_shape && !uniform_qk && cb_k == cb_v && (tile_n == 0 || tile_n == plan_tn) &&
+        g_allow_fused) {
+        int wave_tokens = 0, nsf = 0;
+        fused_plan(B, H_kv, max_seq_len, &wave_tokens, &nsf);
+        const WsLayout wf = ws_layout(B, H_q, nsf);
+        CDA_REQUIRE(nsf <= ns && wf.total <= w.total, f + ": single-launch plan exceeds the workspace");
+        SplitParams p{};
+        p.q_rot = nullptr;
+        p.kv = static_cast<const uint8_t *>(kv_cache);
+        p.block_table = block_table;
+        p.seq_lens = seq_lens;
+        p.cb_k = cb_k;
+        p.cb_v = cb_v;
+        p.part_o = reinterpret_cast<float *>(ws + wf.part_o);
+        p.part_ml = reinterpret_cast<float *>(ws + wf.part_ml);
+        p.row_bytes = (int64_t)H_kv * slot_bytes;
+        p.bt_stride = bt_stride;
+        p.H_q = H_q;
+        p.H_kv = H_kv;
+        p.slot_bytes = slot_bytes;
+        p.block_size = block_size;
+        p.tile_n = kWaves * wave_tokens;
+        p.n_splits = nsf;
+        p.scale_log2 = scale * kLog2e;
+        p.levels = levels_k;
+        p.q = static_cast<const uint16_t *>(q);
+        p.R = rot_f32;
+        p.out = static_cast<uint16_t *>(out);
+        p.wave_tokens = wave_tokens;
+        const int units = B * nsf;
+        p.xcd_map = (units % 8 == 0) ? 1 : 0;
+        const dim3 grid(units * H_kv);
+        if (g_split_start && hipEventRecord(g_split_start, st) != hipSuccess)
+            return fail(CDA_E_HIP, f + ": hipEventRecord(start) failed");
+        if (levels_k == 16) {
+            if (group_size == 4)
+                decode_stream_kernel<4, 16, false, true><<<grid, kThreads, 0, st>>>(p);
+            else
+                decode_stream_kernel<8, 16, false, true><<<grid, kThreads, 0, st>>>(p);
+        } else {
+            if (group_size == 4)
+                decode_stream_kernel<4, 4, false, true><<<grid, kThreads, 0, st>>>(p);
+            else
+                decode_stream_kernel<8, 4, false, true><<<grid, kThreads, 0, st>>>(p);
+        }
+        CDA_LAUNCH_CHECK("decode_stream_kernel");
+        if (g_split_stop && hipEventRecord(g_split_stop, st) != hipSuccess)
+            return fail(CDA_E_HIP, f + ": hipEventRecord(stop) failed");
+        if (nsf > 1) {
+            if ((int64_t)head_grid.x * B < num_cus())
+                combine_kernel<1><<<dim3(H_q, B), 256, 0, st>>>(p.part_o, p.part_ml, rot_f32,
+                                                                p.out, H_q, nsf);
+            else
+                combine_kernel<4><<<head_grid, 256, 0, st>>>(p.part_o, p.part_ml, rot_f32,
+                                                             p.out, H_q, nsf);
+            CDA_LAUNCH_CHECK("combine_kernel");
+        }
+        return CDA_OK;
+    }
     const bool dual = stream_shape && cb_k != cb_v && !uniform_qk;
     int *cb_same = dual ? reinterpret_cast<int *>(ws + w.flag) : nullptr;
     int *k_uniform = uniform_qk ? reinterpret_cast<int *>(ws + w.flag) + 1 : nullptr;
@@ -1535,6 +1777,11 @@ extern "C" int cda_decode_set_timing_events(void *start_event, void *stop_event)
 
 extern "C" int cda_decode_set_stream_kernel(int enable) {
     g_allow_stream = enable != 0;
+    return CDA_OK;
+}
+
+extern "C" int cda_decode_set_fused_kernel(int enable) {
+    g_allow_fused = enable != 0;
     return CDA_OK;
 }
 

@@ -284,3 +284,93 @@ def test_decode_capture_first(gpu, same_values):
         g.replay()
         torch.cuda.synchronize()
         check(out.cpu().numpy(), case.expected)
+
+
+def _plan_fused(B, n, cus=256):
+    """Host restatement of the single-launch plan (splits per sequence), to
+    label the cases below by the path they take."""
+    n = max(n, 1)
+    s = max(1, min(-(-cus // (8 * B)), -(-n // 512)))
+    s = max(s, -(-n // 65536))
+    wg = -(-(-(-n // s)) // 512) * 512
+    return -(-n // wg)
+
+
+FUSED_CASES = [
+    # name, seq_lens, gs, levels, block_size
+    ("b8_xcd_combine", [700, 64, 1, 4096, 300, 2049, 65, 1000], 4, 16, 16),
+    ("b3_combine", [5000, 17, 900], 4, 16, 16),
+    ("b1_long_combine", [20000], 4, 16, 16),
+    ("b32_single_launch", [int(x) for x in np.random.default_rng(7).integers(1, 1600, 32)],
+     4, 16, 16),
+    ("b32_gs8_single_launch", [int(x) for x in np.random.default_rng(8).integers(1, 900, 32)],
+     8, 16, 32),
+    ("b5_empty_mixed", [0, 513, 0, 64, 1], 4, 16, 16),
+    ("b32_k2v2_single_launch", [int(x) for x in np.random.default_rng(9).integers(1, 1300, 32)],
+     4, 4, 16),
+    ("b2_k2v2_gs8_combine", [3000, 777], 8, 4, 16),
+]
+
+
+@pytest.mark.parametrize("name,seq_lens,gs,levels,bs", FUSED_CASES,
+                         ids=[c[0] for c in FUSED_CASES])
+def test_decode_single_launch_matches_checker(gpu, codebooks, name, seq_lens, gs, levels, bs):
+    """The single-launch decode (one workgroup per sequence x split x KV head:
+    in-kernel q rotation, eight waves on consecutive token ranges merged in
+    LDS, the R^T epilogue in the kernel when one split covers the sequence,
+    the combine launch otherwise) against the checker, and against the
+    three-launch form on the same inputs."""
+    from sub0_amd import _native
+    B, n = len(seq_lens), max(seq_lens)
+    print(f"[decode-fused] case={name} B={B} max_n={n} gs={gs} levels={levels} bs={bs} "
+          f"splits={_plan_fused(B, n)}", flush=True)
+    cb = None if levels == 16 else codebooks["lloyd_beta4"].astype(np.float32)
+    case = make_decode_case(7000 + len(name), seq_lens, H_kv=8, gs=gs, block_size=bs, cb=cb,
+                            fill=0xFF)
+    fused = run_gpu_decode(case, gpu, gs=gs)
+    _native.set_fused_kernel(False)
+    try:
+        three = run_gpu_decode(case, gpu, gs=gs)
+    finally:
+        _native.set_fused_kernel(True)
+    for b in range(B):
+        if seq_lens[b] == 0:
+            assert np.all(fused[b] == 0)
+    check(fused, case.expected)
+    check(three, case.expected)
+    check(fused, three, tol=1e-3)
+
+
+@pytest.mark.parametrize("seq_lens", [[1500] * 32, [9000, 3]], ids=["single", "combine"])
+def test_decode_single_launch_graph_replay(gpu, seq_lens):
+    """The single-launch decode captured in a graph: every replay equals the
+    eager output."""
+    case = make_decode_case(7100 + len(seq_lens), seq_lens, H_kv=8, gs=4, fill=0xFF)
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(gpu)
+    q, cache, bt, sl, cb, R = (t(case.q), t(case.cache), t(case.block_table),
+                               t(case.seq_lens), t(case.cb_k), t(case.R))
+    out = torch.full_like(q, float("nan"))
+    from sub0_amd import _native
+
+    def call():
+        _native.decode(q, cache, bt, sl, cb, cb, R, R.half(), out, group_size=4, block_size=16,
+                       tile_n=0, max_seq_len=max(seq_lens), scale=float(1 / np.sqrt(128)))
+
+    call()
+    torch.cuda.synchronize()
+    eager = out.clone()
+    check(eager.cpu().numpy(), case.expected)
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        call()
+        with torch.cuda.graph(g, stream=s):
+            call()
+    torch.cuda.current_stream().wait_stream(s)
+    for _ in range(3):
+        out.fill_(float("nan"))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager)
