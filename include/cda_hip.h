@@ -66,6 +66,13 @@ const char *cda_hip_last_error(void);
 int cda_decode_plan(int B, int H_q, int H_kv, int max_seq_len, int tile_n, int *tile_n_out,
                     int *n_splits_out);
 size_t cda_decode_workspace_size(int B, int H_q, int H_kv, int max_seq_len, int tile_n);
+/* Plan of the single-launch decode (no reference counterpart; the reference's
+ * wrapper only sizes tile_N): workgroups of one KV head over 8 * wave_tokens
+ * context tokens, n_splits per sequence.  wave_tokens is a multiple of 64,
+ * 8 * wave_tokens <= 65536, and n_splits never exceeds cda_decode_plan's for
+ * the same shape, so the single launch fits cda_decode_workspace_size(). */
+int cda_decode_fused_plan(int B, int H_kv, int max_seq_len, int *wave_tokens_out,
+                          int *n_splits_out);
 int cda_decode_full_hmma_v3(const void *q, const void *kv_cache, int64_t num_slots,
                             int slot_bytes, int H_kv, const int32_t *block_table,
                             int bt_stride, const int32_t *seq_lens, const float *cb_k,

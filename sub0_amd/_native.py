@@ -29,6 +29,7 @@ SYMBOLS = (
     "cda_decode_set_timing_events",
     "cda_decode_set_stream_kernel",
     "cda_decode_set_fused_kernel",
+    "cda_decode_fused_plan",
     "cda_decode_full_hmma_v3_k4v2",
     "cda_paged_encode_fused_k4v2",
     "cda_fa2_paged_cache_to_dense_rotated_k4v2",
@@ -106,6 +107,9 @@ def lib():
         L.cda_decode_set_stream_kernel.argtypes = [_I32]
         L.cda_decode_set_fused_kernel.restype = _I32
         L.cda_decode_set_fused_kernel.argtypes = [_I32]
+        L.cda_decode_fused_plan.restype = _I32
+        L.cda_decode_fused_plan.argtypes = [_I32, _I32, _I32, ctypes.POINTER(_I32),
+                                            ctypes.POINTER(_I32)]
         L.cda_decode_full_hmma_v3_k4v2.restype = _I32
         L.cda_decode_full_hmma_v3_k4v2.argtypes = [
             _P, _P, _I64, _I32, _I32, _P, _I32, _P, _P, _P, _P, _P, _P,
@@ -196,6 +200,14 @@ def decode_plan(B: int, H_q: int, H_kv: int, max_seq_len: int, tile_n: int = 0):
     _check(lib().cda_decode_plan(B, H_q, H_kv, max_seq_len, tile_n, ctypes.byref(tn),
                                  ctypes.byref(ns)), "cda_decode_plan")
     return tn.value, ns.value
+
+
+def decode_fused_plan(B: int, H_kv: int, max_seq_len: int) -> tuple[int, int]:
+    """(wave_tokens, n_splits) of the single-launch decode."""
+    wt, ns = _I32(), _I32()
+    _check(lib().cda_decode_fused_plan(B, H_kv, max_seq_len, ctypes.byref(wt), ctypes.byref(ns)),
+           "cda_decode_fused_plan")
+    return wt.value, ns.value
 
 
 def decode_workspace_size(B: int, H_q: int, H_kv: int, max_seq_len: int, tile_n: int = 0) -> int:

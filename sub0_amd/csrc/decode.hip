@@ -1504,6 +1504,17 @@ extern "C" int cda_decode_plan(int B, int H_q, int H_kv, int max_seq_len, int ti
     return CDA_OK;
 }
 
+extern "C" int cda_decode_fused_plan(int B, int H_kv, int max_seq_len, int *wave_tokens_out,
+                                     int *n_splits_out) {
+    if (B <= 0 || H_kv <= 0 || max_seq_len < 0)
+        return fail(CDA_E_INVALID, "cda_decode_fused_plan: B, H_kv must be > 0 and max_seq_len >= 0");
+    int wt = 0, ns = 0;
+    fused_plan(B, H_kv, max_seq_len, &wt, &ns);
+    if (wave_tokens_out) *wave_tokens_out = wt;
+    if (n_splits_out) *n_splits_out = ns;
+    return CDA_OK;
+}
+
 extern "C" size_t cda_decode_workspace_size(int B, int H_q, int H_kv, int max_seq_len,
                                             int tile_n) {
     int tn = 0, ns = 0;

@@ -38,6 +38,31 @@ def test_version_and_plan():
     assert 0 < ws1 <= ws2 and ws1 % 256 == 0
 
 
+def test_decode_fused_plan_fits_the_workspace():
+    """The single-launch plan (256 CUs without a device): whole 64-token
+    chunks per wave, at most 4096 pages per workgroup, every token covered,
+    and never more splits than the three-launch plan, whose
+    cda_decode_workspace_size() callers allocate."""
+    from sub0_amd import _native
+    assert _native.decode_fused_plan(32, 8, 65536) == (8192, 1)     # one launch per step
+    assert _native.decode_fused_plan(32, 8, 4096) == (512, 1)
+    assert _native.decode_fused_plan(1, 8, 4096) == (64, 8)         # one chunk per wave
+    assert _native.decode_fused_plan(1, 8, 65536) == (256, 32)
+    assert _native.decode_fused_plan(4, 8, 65536) == (1024, 8)
+    assert _native.decode_fused_plan(32, 8, 262144) == (8192, 4)    # page-row table cap
+    assert _native.decode_fused_plan(3, 8, 0) == (64, 1)
+    for B in (1, 2, 3, 4, 5, 7, 8, 16, 31, 32, 64, 256):
+        for n in (1, 63, 64, 65, 511, 512, 513, 1000, 4096, 16383, 16384, 65535, 65536,
+                  65537, 131072, 262144, 1000003):
+            wt, ns = _native.decode_fused_plan(B, 8, n)
+            assert wt % 64 == 0 and 64 <= 8 * wt <= 65536, (B, n, wt)
+            assert 8 * wt * ns >= n and 8 * wt * (ns - 1) < n, (B, n, wt, ns)
+            _, ns3 = _native.decode_plan(B, 8 * 4, 8, n)
+            assert ns <= ns3, (B, n, ns, ns3)
+    with pytest.raises(ValueError):
+        _native.decode_fused_plan(0, 8, 100)
+
+
 def test_prefill_key_split_plan():
     """Host-side plan of the key-split prefill: split only short chunks over
     long contexts (grid under 256 workgroups, >= 4 key tiles per split, <= 64
