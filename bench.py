@@ -1142,7 +1142,9 @@ def main(argv=None):
                            pct_peak=round(100 * nb2 / (us * 1e-6) / 1e9 / PEAK_GBS, 1),
                            split_kernel_us=round(kus, 2),
                            split_gbs=round(nb2 / (kus * 1e-6) / 1e9, 1),
-                           bytes=nb2, tile_n=_native.decode_plan(sb, H_Q, H_KV, sn)[0])
+                           bytes=nb2, tile_n=_native.decode_plan(sb, H_Q, H_KV, sn)[0],
+                           single_launch_splits=(None if args.three_launch else
+                                                 _native.decode_fused_plan(sb, H_KV, sn)[1]))
                 log(json.dumps(row))
                 sweep.append(row)
                 del g2
@@ -1200,7 +1202,10 @@ def main(argv=None):
                                   else "Llama-3-8B heads (32 Q / 8 KV")
                                + ", d=128), block 16",
                    "B": B, "N": N, "H_q": H_Q, "H_kv": H_KV, "head_dim": D, "block_size": BS,
-                   "tile_n": tile, "splits": splits, "algorithmic_bytes": nbytes},
+                   "tile_n": tile, "splits": splits, "algorithmic_bytes": nbytes,
+                   **({"single_launch": dict(zip(("wave_tokens", "splits"),
+                                                 _native.decode_fused_plan(B, H_KV, N)))}
+                      if kernel == "decode_stream_kernel<FUSED>" else {})},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / PEAK_GBS, 4),
                      "traffic": traffic, "traffic_measured_at": traffic_at, "kernel": kernel,
