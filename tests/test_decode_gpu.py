@@ -309,6 +309,9 @@ FUSED_CASES = [
     ("b32_k2v2_single_launch", [int(x) for x in np.random.default_rng(9).integers(1, 1300, 32)],
      4, 4, 16),
     ("b2_k2v2_gs8_combine", [3000, 777], 8, 4, 16),
+    ("b3_block48_combine", [2500, 48, 1100], 4, 16, 48),
+    ("b32_block64_single_launch", [int(x) for x in np.random.default_rng(10).integers(1, 1000, 32)],
+     4, 16, 64),
 ]
 
 
@@ -374,3 +377,13 @@ def test_decode_single_launch_graph_replay(gpu, seq_lens):
         g.replay()
         torch.cuda.synchronize()
         assert torch.equal(out, eager)
+
+
+def test_decode_single_launch_slack_max_seq_len(gpu):
+    """max_seq_len far above every sequence (the plan covers tokens no
+    sequence has): same result as the tight bound."""
+    case = make_decode_case(7200, [900, 33, 2000], H_kv=8, gs=4, fill=0xFF)
+    tight = run_gpu_decode(case, gpu, gs=4)
+    slack = run_gpu_decode(case, gpu, gs=4, max_seq_len=60000)
+    check(slack, case.expected)
+    check(slack, tight, tol=1e-3)
