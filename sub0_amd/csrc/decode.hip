@@ -495,12 +495,13 @@ decode_split_kernel(SplitParams p) {
 //   [0, 512)      K codes: piece 16*c + t = token t, 16-byte column c (0..1)
 //   [512, 1024)   V codes: token t's 32 bytes at 32 * vslot2(t)
 //   [1024, 1280)  norms, as above
-// The table row e holds (cb[e >> 6], cb[(e >> 4) & 3]): the code pair in the
-// high nibble of e.  A byte of 2-bit codes (dims 4j..4j+3, first dim in bits
-// 7:6) gives dims (4j, 4j+1) from itself and (4j+2, 4j+3) from the same byte
-// of the word shifted left by 4.  For V, two tokens' codes of one dim are
-// first interleaved into one nibble (bit-field inserts), as the K4V4 path
-// pairs two tokens' nibbles into one byte.
+// The table row e (256 B) holds, for 16 lane columns of 16 bytes,
+// (cb[e >> 6], cb[(e >> 4) & 3], cb[(e >> 2) & 3], cb[e & 3]): a byte of
+// 2-bit codes (dims 4j..4j+3, first dim in bits 7:6) gives its four values in
+// one ds_read_b128.  For V, two tokens' codes of one dim are first
+// interleaved into the high nibble of a byte (bit-field inserts), as the K4V4
+// path pairs two tokens' nibbles into one byte, and the first 8 bytes of the
+// entry are read.
 // ---------------------------------------------------------------------------
 
 constexpr int kHeadPage = 16 * 144;      // largest share of one head in a page (K4V4): 2304 B
@@ -746,8 +747,8 @@ decode_stream_kernel(SplitParams p) {
             const int e = i >> 6;
             if constexpr (L == 16)
                 lut[i] = __float_as_uint(cbs[(i & 1) ? (e & 15) : (e >> 4)]);
-            else
-                lut[i] = __float_as_uint(cbs[(i & 1) ? ((e >> 4) & 3) : (e >> 6)]);
+            else   // quad q of row e: the code in bits 7-2q:6-2q (dims 4j + q)
+                lut[i] = __float_as_uint(cbs[(e >> (6 - 2 * (i & 3))) & 3]);
         }
     }
     if constexpr (FUSED) {
@@ -785,7 +786,9 @@ decode_stream_kernel(SplitParams p) {
                           : rb0 + kVo + 32u * vslot2(4 * q4 + i) + 2u * r16;
         oNV[i] = rb0 + kNo + 16u * (4 * q4 + i) + 4u;
     }
-    const uint32_t col = (uint32_t)(lane & 31) * 8u;
+    // Table column of this lane: 32 columns of 8-byte pairs (4-bit codes) or
+    // 16 columns of 16-byte quads (2-bit codes); either way a row is 256 bytes.
+    const uint32_t col = (L == 16) ? (uint32_t)(lane & 31) * 8u : (uint32_t)(lane & 15) * 16u;
     const uint8_t *lutb = smem;
 
     floatx4 acc_o[8];
@@ -838,21 +841,25 @@ decode_stream_kernel(SplitParams p) {
                 cv[4 * s + 3] = CDA_PAIR(3, w[s]);
             }
         } else {
-            // Word x holds dims [16x, 16x+16) of the lane's 32; MFMA s takes
-            // bytes 2s, 2s+1 (dims 8s..8s+7).
+            // Word x holds dims [16x, 16x+16) of the lane's 32, byte k dims
+            // 16x + 4k .. +3; one 16-byte table read per byte gives all four.
+            // MFMA s takes bytes 2s, 2s+1 (dims 8s..8s+7).
             const uint32_t w[2] = {r.kq.x, r.kq.y};
-            const uint32_t sh[2] = {r.kq.x << 4, r.kq.y << 4};
+#define CDA_QUAD(K_, W_) (*reinterpret_cast<const float4 *>(lutb + lut_addr<K_>(W_, col)))
 #pragma unroll
             for (int x = 0; x < 2; ++x) {
-                cv[8 * x + 0] = CDA_PAIR(0, w[x]);
-                cv[8 * x + 1] = CDA_PAIR(0, sh[x]);
-                cv[8 * x + 2] = CDA_PAIR(1, w[x]);
-                cv[8 * x + 3] = CDA_PAIR(1, sh[x]);
-                cv[8 * x + 4] = CDA_PAIR(2, w[x]);
-                cv[8 * x + 5] = CDA_PAIR(2, sh[x]);
-                cv[8 * x + 6] = CDA_PAIR(3, w[x]);
-                cv[8 * x + 7] = CDA_PAIR(3, sh[x]);
+                const float4 q0 = CDA_QUAD(0, w[x]), q1 = CDA_QUAD(1, w[x]);
+                const float4 q2 = CDA_QUAD(2, w[x]), q3 = CDA_QUAD(3, w[x]);
+                cv[8 * x + 0] = make_float2(q0.x, q0.y);
+                cv[8 * x + 1] = make_float2(q0.z, q0.w);
+                cv[8 * x + 2] = make_float2(q1.x, q1.y);
+                cv[8 * x + 3] = make_float2(q1.z, q1.w);
+                cv[8 * x + 4] = make_float2(q2.x, q2.y);
+                cv[8 * x + 5] = make_float2(q2.z, q2.w);
+                cv[8 * x + 6] = make_float2(q3.x, q3.y);
+                cv[8 * x + 7] = make_float2(q3.z, q3.w);
             }
+#undef CDA_QUAD
         }
     };
     // fp16(centroid * norm) of those pairs and the page's QK MFMAs.
