@@ -498,10 +498,9 @@ decode_split_kernel(SplitParams p) {
 // The table row e (256 B) holds, for 16 lane columns of 16 bytes,
 // (cb[e >> 6], cb[(e >> 4) & 3], cb[(e >> 2) & 3], cb[e & 3]): a byte of
 // 2-bit codes (dims 4j..4j+3, first dim in bits 7:6) gives its four values in
-// one ds_read_b128.  For V, two tokens' codes of one dim are first
-// interleaved into the high nibble of a byte (bit-field inserts), as the K4V4
-// path pairs two tokens' nibbles into one byte, and the first 8 bytes of the
-// entry are read.
+// one ds_read_b128.  For V, four tokens' codes of one dim are first
+// gathered into one byte (bit-field inserts), so one read likewise gives the
+// four tokens' values of that dim.
 // ---------------------------------------------------------------------------
 
 constexpr int kHeadPage = 16 * 144;      // largest share of one head in a page (K4V4): 2304 B
@@ -926,28 +925,41 @@ decode_stream_kernel(SplitParams p) {
             CDA_V_TILE(3, ev, 6)
             CDA_V_TILE(3, od, 7)
         } else {
-            // Tokens a = 2*m2, b = 2*m2 + 1 (16 bits each: dims 8*r16 .. +7).
-            // t's nibbles pair (a, b) codes of dims 0, 2 | 4, 6 (bytes 0 | 1),
-            // u's of dims 1, 3 | 5, 7; ev = t | (t << 20) puts the dims 2, 6
-            // nibbles high in bytes 2, 3 (od likewise for u).  Bytes of
-            // ev: dims 0, 4, 2, 6; of od: dims 1, 5, 3, 7.
+            // Four tokens' 2-bit codes of one dim in one byte, first token in
+            // bits 7:6 (the quad table's order), so one 16-byte read gives
+            // the four k slots of a page.  A token's 16 bits (read little
+            // endian) hold dims 8*r16 .. +3 in byte 0 and +4 .. +7 in byte 1,
+            // the first dim of each byte in bits 7:6.  t01 pairs tokens 0, 1
+            // into nibbles (byte 0: dims 0 | 2, byte 1: dims 4 | 6), u01 the
+            // odd dims; then two nibble inserts give (dim 0 | dim 4),
+            // (dim 1 | dim 5), (dim 2 | dim 6), (dim 3 | dim 7) in bytes 0 | 1
+            // of four words.
+            auto quads = [&](const PageRegs &rr, uint32_t (&qw)[4]) CDA_INLINE {
+                const uint32_t v0 = rr.vw[0], v1 = rr.vw[1], v2 = rr.vw[2], v3 = rr.vw[3];
+                const uint32_t t01 = bfi(0xCCCCu, v0, v1 >> 2), u01 = bfi(0xCCCCu, v0 << 2, v1);
+                const uint32_t t23 = bfi(0xCCCCu, v2, v3 >> 2), u23 = bfi(0xCCCCu, v2 << 2, v3);
+                qw[0] = bfi(0xF0F0u, t01, t23 >> 4);          // dims 0 (byte 0), 4 (byte 1)
+                qw[1] = bfi(0xF0F0u, u01, u23 >> 4);          // dims 1, 5
+                qw[2] = bfi(0xF0F0u, t01 << 4, t23);          // dims 2, 6
+                qw[3] = bfi(0xF0F0u, u01 << 4, u23);          // dims 3, 7
+            };
+            uint32_t qa[4], qbw[4];
+            quads(ra, qa);
+            quads(rb, qbw);
+#define CDA_QUAD(K_, W_) (*reinterpret_cast<const float4 *>(lutb + lut_addr<K_>(W_, col)))
 #pragma unroll
-            for (int x = 0; x < 4; ++x) {
-                const PageRegs &rr = (x < 2) ? ra : rb;
-                const uint32_t a = rr.vw[2 * (x & 1)], bb = rr.vw[2 * (x & 1) + 1];
-                const uint32_t t = bfi(0xCCCCu, a, bb >> 2);
-                const uint32_t u = bfi(0xCCCCu, a << 2, bb);
-                ev[x] = t | (t << 20);
-                od[x] = u | (u << 20);
+            for (int j = 0; j < 8; ++j) {
+                // dim j: word j & 3, byte 0 for j < 4, byte 1 otherwise
+                const float4 a4 = (j < 4) ? CDA_QUAD(0, qa[j & 3]) : CDA_QUAD(1, qa[j & 3]);
+                const float4 b4 = (j < 4) ? CDA_QUAD(0, qbw[j & 3]) : CDA_QUAD(1, qbw[j & 3]);
+                vc[4 * j + 0] = make_float2(a4.x, a4.y);
+                vc[4 * j + 1] = make_float2(a4.z, a4.w);
+                vc[4 * j + 2] = make_float2(b4.x, b4.y);
+                vc[4 * j + 3] = make_float2(b4.z, b4.w);
             }
-            CDA_V_TILE(0, ev, 0)
-            CDA_V_TILE(0, od, 1)
-            CDA_V_TILE(2, ev, 2)
-            CDA_V_TILE(2, od, 3)
-            CDA_V_TILE(1, ev, 4)
-            CDA_V_TILE(1, od, 5)
-            CDA_V_TILE(3, ev, 6)
-            CDA_V_TILE(3, od, 7)
+#undef CDA_QUAD
+            (void)ev;
+            (void)od;
         }
 #undef CDA_V_TILE
         // The 32 table reads above all issue before the first multiply.
