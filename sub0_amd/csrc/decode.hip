@@ -4,7 +4,15 @@
 // cda/kernels_cuda/wrappers.py:79-124; math of cda/algorithm/attention.py:
 // 426-482 (attention_compressed), split-K partials and merge of :190-272.
 //
-// Three launches on the caller's stream:
+// Default form, one launch (decode_stream_kernel<..., FUSED = true>): where
+// the page-streaming kernel applies (8 KV heads, 144- or 80-byte slots, one
+// codebook pointer, the library's split plan), one workgroup per (sequence,
+// context split, KV head) rotates that head's GQA group of q, streams the
+// head's pages on eight waves over consecutive token ranges, merges the
+// waves' partials in LDS and, when one split covers the sequence, applies
+// R^T and writes out; with several splits the combine launch follows.
+//
+// Otherwise three launches on the caller's stream:
 //   1. rotate_q:  q_rot = fp16(q @ R) per (b, q-head).
 //   2. split:     one workgroup per (b, context split, group of 8 KV heads);
 //                 wave w owns KV head 8*blockIdx.y + w and its GQA group.  Two
