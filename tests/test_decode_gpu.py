@@ -387,3 +387,21 @@ def test_decode_single_launch_slack_max_seq_len(gpu):
     slack = run_gpu_decode(case, gpu, gs=4, max_seq_len=60000)
     check(slack, case.expected)
     check(slack, tight, tol=1e-3)
+
+
+def test_decode_single_launch_all_empty(gpu):
+    """Every sequence empty and max_seq_len 0: the single launch writes zeros."""
+    case = make_decode_case(7300, [0, 0, 0], H_kv=8, gs=4)
+    out = run_gpu_decode(case, gpu, gs=4, max_seq_len=0)
+    assert np.all(out == 0)
+
+
+def test_decode_single_launch_two_rounds(gpu):
+    """B=64: 512 single-split workgroups, two per CU over the run (the XCD
+    mapping over 64 sequences)."""
+    from sub0_amd import _native
+    rng = np.random.default_rng(11)
+    seq = [int(x) for x in rng.integers(1, 700, 64)]
+    assert _native.decode_fused_plan(64, 8, max(seq))[1] == 1
+    case = make_decode_case(7400, seq, H_kv=8, gs=4, fill=0xFF)
+    check(run_gpu_decode(case, gpu, gs=4), case.expected)
