@@ -5,8 +5,9 @@ The reference resolves each logical kernel name to a prebuilt CUDA ``.so``
 library, ``sub0_amd/_lib/libcda_hip.so``, reached through its C ABI.
 ``load_pybind_module(name)`` returns a module object whose attributes have
 the reference's positional signatures and call the ``torch.ops.cda_hip``
-ops; ``load_torch_ops_library(name)`` returns the registered torch.ops
-namespace (``cda_hip``, or the FA2-fork comparator namespace
+ops; ``load_torch_ops_library(name)`` loads the native ``TORCH_LIBRARY`` build,
+``sub0_amd/_lib/libcda_hip_torch.so``, with ``torch.ops.load_library`` and
+returns the namespace (``cda_hip``, or the FA2-fork comparator namespace
 ``_cda_vllm_fa2_fork_C``; see :mod:`sub0_amd.cda._torch_ops`).  Both are
 ``lru_cache``d and idempotent, and raise :class:`PrebuiltMissing` (an ``ImportError``) when the artefact is
 missing or the name is not provided, as the reference does
@@ -87,7 +88,12 @@ def _make_encode_module(name: str) -> ModuleType:
 
 
 def _register_ops():
-    from sub0_amd.cda import _torch_ops  # noqa: F401  -- registers torch.ops.cda_hip
+    """Load libcda_hip_torch.so (torch.ops.cda_hip and the fork namespace)."""
+    try:
+        from sub0_amd.cda import _torch_ops
+        _torch_ops.load()
+    except _native.NativeMissing as e:
+        raise PrebuiltMissing(str(e)) from e
 
 
 def _factories():
@@ -124,10 +130,11 @@ def load_pybind_module(name: str) -> ModuleType:
 def load_torch_ops_library(name: str):
     """TORCH_LIBRARY flavour (reference ``_prebuilt_loader.py:69-80``): the
     torch.ops namespace ``name`` once its ops are registered."""
-    from sub0_amd.cda import _torch_ops
-    if name not in _torch_ops.NAMESPACES:
+    namespaces = ("cda_hip", "_cda_vllm_fa2_fork_C")
+    if name not in namespaces:
         raise PrebuiltMissing(
             f"torch.ops library '{name}' is not provided by the MI355X build "
-            f"(available: {list(_torch_ops.NAMESPACES)}).")
+            f"(available: {list(namespaces)}).")
     _lib_or_raise()
+    _register_ops()
     return getattr(torch.ops, name)

@@ -33,6 +33,7 @@
 //                 and writes fp16 out.
 #include "cda_common.h"
 
+#include <atomic>
 #include <mutex>
 #include <string>
 #include <type_traits>
@@ -1458,10 +1459,12 @@ WsLayout ws_layout(int B, int H_q, int n_splits) {
 thread_local hipEvent_t g_split_start = nullptr;
 thread_local hipEvent_t g_split_stop = nullptr;
 // Lets tests run the general kernel on shapes the streaming kernel also covers.
-bool g_allow_stream = true;
+// (Process-wide switches; atomics, since another thread may set them while a
+// call reads them.)
+std::atomic<bool> g_allow_stream{true};
 // Lets tests and benchmarks run the three-launch form where the single-launch
 // form also applies.
-bool g_allow_fused = true;
+std::atomic<bool> g_allow_fused{true};
 
 int num_cus() {
     static int cached = 0;
@@ -1602,7 +1605,8 @@ int decode_impl(const void *q, const void *kv_cache, int slot_bytes, int H_kv,
     const bool stream_shape = H_kv == 8 && levels_k == levels_v &&
                               ((levels_k == 16 && slot_bytes == 144) ||
                                (levels_k == 4 && slot_bytes == 80)) &&
-                              tn <= 16 * kStreamMaxPages && g_allow_stream;
+                              tn <= 16 * kStreamMaxPages &&
+                              g_allow_stream.load(std::memory_order_relaxed);
     if (uniform_qk)
         CDA_REQUIRE(stream_shape && levels_k == 16,
                     f + ": the score-domain QK runs on the page-streaming kernel: K4V4 "
@@ -1615,7 +1619,7 @@ int decode_impl(const void *q, const void *kv_cache, int slot_bytes, int H_kv,
     int plan_tn = 0;
     cda_decode_plan(B, H_q, H_kv, max_seq_len, 0, &plan_tn, nullptr);
     if (stream_shape && !uniform_qk && cb_k == cb_v && (tile_n == 0 || tile_n == plan_tn) &&
-        g_allow_fused) {
+        g_allow_fused.load(std::memory_order_relaxed)) {
         int wave_tokens = 0, nsf = 0;
         fused_plan(B, H_kv, max_seq_len, &wave_tokens, &nsf);
         const WsLayout wf = ws_layout(B, H_q, nsf);
@@ -1814,12 +1818,12 @@ extern "C" int cda_decode_set_timing_events(void *start_event, void *stop_event)
 }
 
 extern "C" int cda_decode_set_stream_kernel(int enable) {
-    g_allow_stream = enable != 0;
+    g_allow_stream.store(enable != 0, std::memory_order_relaxed);
     return CDA_OK;
 }
 
 extern "C" int cda_decode_set_fused_kernel(int enable) {
-    g_allow_fused = enable != 0;
+    g_allow_fused.store(enable != 0, std::memory_order_relaxed);
     return CDA_OK;
 }
 

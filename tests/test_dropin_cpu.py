@@ -160,3 +160,39 @@ def test_fa2_fork_interface_rejects_unsupported():
         F.dequantize_compressed_kv(ki[0], kn[0], ki[0], kn[0], cb, cb)
     with pytest.raises(ImportError):
         F.register_vllm_backend()
+
+
+def test_native_torch_library_loads_standalone():
+    """libcda_hip_torch.so is a TORCH_LIBRARY build: a process that never
+    imports this package gets both namespaces from torch.ops.load_library
+    alone (as the reference's load_torch_ops_library does,
+    _prebuilt_loader.py:69-80), with the in-place schemas, the C++ argument
+    checks (TypeError / ValueError before any GPU work) and Meta kernels."""
+    import subprocess
+    import sys
+    from pathlib import Path
+    lib = Path(__file__).resolve().parents[1] / "sub0_amd" / "_lib" / "libcda_hip_torch.so"
+    code = f"""
+import torch
+torch.ops.load_library({str(lib)!r})
+s = str(torch.ops.cda_hip.decode.default._schema)
+assert s.startswith("cda_hip::decode(") and "Tensor(a!) out" in s, s
+assert "Tensor(a!)? out" in str(torch.ops._cda_vllm_fa2_fork_C.varlen_fwd.default._schema)
+q = torch.zeros(2, 32, 128, dtype=torch.float32)
+try:
+    torch.ops.cda_hip.hadamard128(q, q, 1.0)
+except (TypeError, ValueError, NotImplementedError, RuntimeError) as e:
+    print("ERR", type(e).__name__)
+with torch.device("meta"):
+    kv = torch.empty(64, 8, 144, dtype=torch.uint8)
+    bt = torch.empty(2, 4, dtype=torch.int32)
+    sl = torch.empty(2, dtype=torch.int32)
+    cb = torch.empty(16)
+    k, v = torch.ops.cda_hip.paged_to_dense(kv, bt, sl, cb, cb, 16, 40)
+    assert k.shape == (80, 8, 128) and k.dtype == torch.float16
+print("OK")
+"""
+    r = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, timeout=300)
+    assert r.returncode == 0, r.stderr[-2000:]
+    # A CPU tensor has no CUDA kernel: the dispatcher refuses it (no CPU path).
+    assert "ERR NotImplementedError" in r.stdout and r.stdout.strip().endswith("OK"), r.stdout
