@@ -589,6 +589,13 @@ decode_stream_kernel(SplitParams p) {
     static_assert(L == 16 || L == 4, "4-bit or 2-bit codes");
     static_assert(!SQK || L == 16, "score-domain QK: 4-bit K codes");
     static_assert(!(SQK && FUSED), "the score-domain form runs as three launches");
+    static_assert(GS == 4 || GS == 8, "GQA groups of 4 or 8");
+    // The MFMA's 16 score columns hold the GS heads RP times over, so every
+    // lane holds every score of its head RP times.  Each lane computes the
+    // softmax weights of its own share only -- pages g_own + RP*j (j < NPL),
+    // g_own = r16 / GS -- and the weights are exchanged before PV.
+    constexpr int RP = 16 / GS;
+    constexpr int NPL = 4 / RP;
     __shared__ __align__(16) uint8_t smem[FUSED ? kFusedLds : kStreamLds];
     constexpr int S = (L == 16) ? 144 : 80;        // slot bytes
     constexpr int KB = (L == 16) ? 64 : 32;        // code bytes per role
@@ -798,6 +805,7 @@ decode_stream_kernel(SplitParams p) {
     // 16 columns of 16-byte quads (2-bit codes); either way a row is 256 bytes.
     const uint32_t col = (L == 16) ? (uint32_t)(lane & 31) * 8u : (uint32_t)(lane & 15) * 16u;
     const uint8_t *lutb = smem;
+    const int g_own = r16 / GS;
 
     floatx4 acc_o[8];
 #pragma unroll
@@ -1079,26 +1087,44 @@ decode_stream_kernel(SplitParams p) {
                 for (int i = 0; i < 4; ++i) acc_o[j][i] *= f[i];
         }
         const float m_sub = (m_run == -INFINITY) ? 0.0f : m_run;
-        float pv[4][4];
+        // Softmax weights of the lane's own share (page g_own + RP*j, token
+        // 4*q4 + i), as fp16 pairs.
+        uint32_t pw[NPL][2];
         float psum = 0.0f;
 #pragma unroll
-        for (int k = 0; k < 4; ++k)
+        for (int j = 0; j < NPL; ++j) {
+            float pj[4];
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const float pr = __builtin_amdgcn_exp2f(fmaf(raw[k][i], p.scale_log2, -m_sub));
+                float sv = raw[j * RP][i];
+#pragma unroll
+                for (int t = 1; t < RP; ++t) sv = (g_own == t) ? raw[j * RP + t][i] : sv;
+                const float pr = __builtin_amdgcn_exp2f(fmaf(sv, p.scale_log2, -m_sub));
                 psum += pr;
-                pv[k][i] = (MASK && c0 + 16 * k + 4 * q4 + i >= wend) ? 0.0f : pr;
+                pj[i] = (MASK && c0 + 16 * (j * RP + g_own) + 4 * q4 + i >= wend) ? 0.0f : pr;
             }
+            pw[j][0] = cvt_pk_rn(pj[0], pj[1]);
+            pw[j][1] = cvt_pk_rn(pj[2], pj[3]);
+        }
         l_run += psum;
-        uint4 pa0, pa1;
-        pa0.x = cvt_pk_rn(pv[0][0], pv[0][1]);
-        pa0.y = cvt_pk_rn(pv[0][2], pv[0][3]);
-        pa0.z = cvt_pk_rn(pv[1][0], pv[1][1]);
-        pa0.w = cvt_pk_rn(pv[1][2], pv[1][3]);
-        pa1.x = cvt_pk_rn(pv[2][0], pv[2][1]);
-        pa1.y = cvt_pk_rn(pv[2][2], pv[2][3]);
-        pa1.z = cvt_pk_rn(pv[3][0], pv[3][1]);
-        pa1.w = cvt_pk_rn(pv[3][2], pv[3][3]);
+        // Page kk's weights of head r16 % GS are in lane (kk % RP) * GS +
+        // r16 % GS of this 16-lane row, register kk / RP: ds_swizzle in
+        // bit-mask mode keeps the head and row bits and sets the page bits.
+        constexpr int kGMask = (RP - 1) * GS;
+        uint32_t xw[4][2];
+#define CDA_SWZ(KK_)                                                                    \
+    {                                                                                   \
+        constexpr int pat = (0x1F & ~kGMask) | ((((KK_) % RP) * GS) << 5);              \
+        xw[KK_][0] = (uint32_t)__builtin_amdgcn_ds_swizzle((int)pw[(KK_) / RP][0], pat); \
+        xw[KK_][1] = (uint32_t)__builtin_amdgcn_ds_swizzle((int)pw[(KK_) / RP][1], pat); \
+    }
+        CDA_SWZ(0)
+        CDA_SWZ(1)
+        CDA_SWZ(2)
+        CDA_SWZ(3)
+#undef CDA_SWZ
+        const uint4 pa0 = make_uint4(xw[0][0], xw[0][1], xw[1][0], xw[1][1]);
+        const uint4 pa1 = make_uint4(xw[2][0], xw[2][1], xw[3][0], xw[3][1]);
         if (MASK) {
             // A masked token's V is zeroed: its slot may hold garbage norms.
 #pragma unroll
@@ -1122,7 +1148,11 @@ decode_stream_kernel(SplitParams p) {
     }
     if (nfull < nchunks) step(nfull, std::true_type{});
 
-    const float l = rows_sum(l_run);
+    // Each lane summed its own share: add the other pages' lanes of its row.
+    float l = rows_sum(l_run);
+    if constexpr (GS == 4)
+        l += __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(l), 0x1F | (4 << 10)));
+    l += __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(l), 0x1F | (8 << 10)));
     if constexpr (FUSED) {
         // Merge the eight waves' partials of this head's GQA group
         // (attention.py:239-272, log2 domain).  Each wave parks its (O, m, l)
