@@ -16,12 +16,17 @@ line on stdout.
 * ``value`` = algorithmic HBM bytes per step / time per step (GB/s); the
   bytes are B*N*8*136 (codes + fp32 norms per token and KV head) + Q/O +
   block-table + seq_lens (``decode_algorithmic_bytes``).
-* ``roofline`` = the same bytes over the split-K kernel's own average
-  duration, measured with HIP events recorded on its launch stream around
-  that kernel only, against MI355X's 8 TB/s.
-* ``cpu_baseline`` = the repository's C restatement of the reference
-  algorithm (oracle/, "port") on BASELINE config 0 (B=1, N=4096: encode K and
-  V, then one decode step), on the host cores.
+* ``roofline`` = the same bytes over the average duration of the kernel
+  that streams the cache (the single-launch decode kernel by default; the
+  split kernel with ``--three-launch``), measured with HIP events recorded on
+  its launch stream around that kernel only, against MI355X's 8 TB/s;
+  ``traffic`` = its calibrated rocprofv3 FETCH_SIZE + WRITE_SIZE bytes.
+* ``cpu_baseline`` = the reference's torch CPU path restated operation for
+  operation (``oracle/torch_ref.py``: compression.py encode +
+  attention.py attention_compressed, "port") on BASELINE config 0 (B=1,
+  N=4096: encode K and V, then one decode step) on the host cores, all
+  threads and one; ``c_checker`` beside it = the C checker
+  (``oracle/cda_oracle.c``) on the same workload.
 ``--sweep`` also times the 3x3 grid B in {1,4,32} x N in {4K,16K,64K} (median
 of 20 graph replays after 5 warm-ups, as the reference's Table 2) and writes
 it to stderr (and as a JSON list to ``--sweep-out PATH`` when given).
@@ -505,6 +510,22 @@ def encode_cpu_baseline(levels: int, tokens: int = 2048, reps: int = 5):
                       f"(oracle/torch_ref.py)"}
 
 
+def _enc_fmas_per_vector(lanes: int = 4, d: int = 128) -> int:
+    """FMAs of paged_encode_kernel's rotation per 128-vector: `lanes` lanes
+    own outputs j = r + lanes*m; for k < lanes every output of a lane has the
+    same Sylvester sign pattern (one chain), and each doubling of k splits the
+    chains in two, so k in [2^i, 2^(i+1)) (2^i >= lanes) runs 2^(i+1)/lanes
+    chains."""
+    per_lane, k = lanes, lanes
+    while k < d:
+        per_lane += k * (2 * k // lanes)
+        k *= 2
+    return per_lane * lanes
+
+
+ENC_FMAS_PER_VECTOR = _enc_fmas_per_vector()
+
+
 def encode_main(args) -> int:
     """--encode: BASELINE config 2 (not the headline metric); one JSON line
     with the K4V4 figures and the K2V2 ones beside them."""
@@ -543,6 +564,8 @@ def encode_main(args) -> int:
     w, ms, k_us = res[16]
     gbs = w["bytes"] / (ms * 1e-3) / 1e9
     k_gbs = w["bytes"] / (k_us * 1e-6) / 1e9
+    enc_flops = 2 * ENC_FMAS_PER_VECTOR * 2 * w["T"] * H_KV
+    k_tflops = enc_flops / (k_us * 1e-6) / 1e12
     w2, ms2, k_us2 = res[4]
     line = {
         "metric": "fused paged encode GB/s of algorithmic bytes (BASELINE config 2)",
@@ -553,10 +576,24 @@ def encode_main(args) -> int:
         "config": {"workload": "64 sequences x U[1,256] new tokens, 8 KV heads, d=128, "
                                "K4V4 (144-byte slots), permuted block table",
                    "tokens": w["T"], "algorithmic_bytes": w["bytes"]},
-        "roofline": {"bound": "hbm", "achieved": round(k_gbs, 1), "peak": 8000.0, "unit": "GB/s",
-                     "frac": round(k_gbs / 8000.0, 4),
-                     **load_kernel_traffic("paged_encode_kernel<16>", "config2"),
-                     "kernel": "paged_encode_kernel<16>", "kernel_us": round(k_us, 2)},
+        # The kernel is bound by VALU issue of the reference-order fp32 fma
+        # chain, not by HBM: its roofline is the fp32 FMA rate.
+        "roofline": {"bound": "valu", "achieved": round(k_tflops, 2), "peak": 157.3,
+                     "unit": "TFLOP/s", "frac": round(k_tflops / 157.3, 4),
+                     "flops_per_launch": enc_flops,
+                     "flops_definition": "executed fp32 FMAs of the rotation chains x 2: "
+                                         f"{ENC_FMAS_PER_VECTOR} FMAs per 128-vector (the chains "
+                                         "of one vector share prefixes), 2 vectors (K, V) per "
+                                         "token and KV head",
+                     "peak_nonpacked": 78.6, "frac_nonpacked": round(k_tflops / 78.6, 4),
+                     "peak_note": "157.3 TFLOP/s needs packed fp32 FMAs (2 per lane per "
+                                  "instruction); this build is compiled without packed fp32 "
+                                  "(-packed-fp32-ops), whose issue peak is 78.6 TFLOP/s "
+                                  "(256 CUs x 4 SIMDs x 16 lanes x 2 flops x 2.4 GHz)",
+                     "kernel": "paged_encode_kernel<16>", "kernel_us": round(k_us, 2),
+                     "hbm": {"achieved": round(k_gbs, 1), "peak": 8000.0, "unit": "GB/s",
+                             "frac": round(k_gbs / 8000.0, 4),
+                             **load_kernel_traffic("paged_encode_kernel<16>", "config2")}},
         "k2v2": {"tokens": w2["T"], "algorithmic_bytes": w2["bytes"], "ms_per_step": round(ms2, 5),
                  "value": round(w2["bytes"] / (ms2 * 1e-3) / 1e9, 1),
                  "kernel_us": round(k_us2, 2),

@@ -136,7 +136,9 @@ int cda_qk_scores_uniform4(const void *q_rot, const void *k_idx, const float *k_
  * cda_decode_noalloc_max_workspace() bytes (16 MiB; held until the process
  * ends).  Shapes whose cda_decode_workspace_size() exceeds it return
  * CDA_E_WORKSPACE.  It calls no allocator.  Calls on one GPU share the
- * array: calls that overlap on one GPU (several streams or threads) race. */
+ * array, so calls that overlap on one GPU are not allowed: serialise them on
+ * one stream (graph replays included); overlapping calls from several
+ * streams or threads race on the partials and give wrong output. */
 size_t cda_decode_noalloc_max_workspace(void);
 int cda_decode_full_hmma_v3_noalloc(const void *q, const void *kv_cache, int64_t num_slots,
                                     int slot_bytes, int H_kv, const int32_t *block_table,

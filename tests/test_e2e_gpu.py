@@ -33,20 +33,29 @@ def test_e2e_gs8_heads(gpu):
 
 def test_e2e_config4_full_size(gpu):
     """BASELINE config 4 at its stated shape: 32 layers, hidden 4096, 32/8
-    heads, SwiGLU 14336, 32 sequences x 16384-token prefix, K4V4 cache, 8
-    greedy steps.  Replayed steps produce the eager steps' tokens, and one
-    layer's decode over its ~16.4K-token cache is within 2e-3 of a float64
-    torch reference on the dense dequantised rows of that cache."""
+    heads, SwiGLU 14336, 32 sequences x 16384-token prefix, K4V4 cache, 256
+    greedy steps (the whole config).  Prints and checks the run's decode
+    tokens/s and attention share; replayed steps produce the eager steps'
+    tokens, and one layer's decode over its ~16.6K-token cache is within 2e-3
+    of a float64 torch reference on the dense dequantised rows of that cache."""
     import bench
     from sub0_amd import _native
-    print("[e2e] config 4: B=32 prefix=16384 steps=8 layers=32", flush=True)
-    r = bench.e2e_run(gpu, B=32, prefix=16384, steps=8, check_eager=3, keep_state=True)
+    steps = 256
+    print(f"[e2e] config 4: B=32 prefix=16384 steps={steps} layers=32", flush=True)
+    r = bench.e2e_run(gpu, B=32, prefix=16384, steps=steps, check_eager=3, keep_state=True)
+    share = r["attn_ms"] / r["step_ms"]
+    print(f"[e2e] config 4: {r['tokens_per_s']:.1f} tokens/s over {r['decode_steps']} decode "
+          f"steps, {r['step_ms']:.3f} ms per step, attention (cache update + attention, "
+          f"32 layers) {r['attn_ms']:.3f} ms = {share:.3f} of the step; prefill "
+          f"{r['prefill_s']:.2f} s", flush=True)
+    assert r["decode_steps"] >= steps - 1 and r["tokens_per_s"] > 0
+    assert 0.0 < share < 1.0
     for i, want in enumerate(r["eager_tokens"]):
         assert torch.equal(r["produced"][2 + i], want), f"replay {i + 1}"
     m, caches, bt = r["model"], r["caches"], r["block_table"]
     lens = r["cached_lens"].to(torch.int32)
     N = int(lens[0])
-    assert bool((lens == N).all()) and N == 16384 + 8
+    assert bool((lens == N).all()) and N == 16384 + steps
     li = 17
     A = m.A
     B, H, Hkv, D = 32, 32, 8, 128
