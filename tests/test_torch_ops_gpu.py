@@ -191,3 +191,40 @@ def test_fork_python_interface(gpu, codebooks, entry):
     torch.cuda.synchronize()
     err = float((out.float() - ref.float()).abs().max())
     assert err <= TOL, err
+
+
+def test_native_ops_error_types(gpu):
+    """The C++ registrations raise the reference wrappers' exception types
+    (wrappers.py:110-113, 143-148) before launching anything: TypeError for
+    dtypes, ValueError for shapes, NotImplementedError for fork features the
+    kernels lack."""
+    from sub0_amd.cda._prebuilt_loader import load_torch_ops_library
+    ops = load_torch_ops_library("cda_hip")
+    fork = load_torch_ops_library("_cda_vllm_fa2_fork_C")
+    q = torch.zeros(2, 32, 128, dtype=torch.float16, device=gpu)
+    kv = torch.zeros(64, 8, 144, dtype=torch.uint8, device=gpu)
+    bt = torch.zeros(2, 4, dtype=torch.int32, device=gpu)
+    sl = torch.full((2,), 40, dtype=torch.int32, device=gpu)
+    cb = torch.zeros(16, device=gpu)
+    R = torch.eye(128, device=gpu)
+    out = torch.empty_like(q)
+    with pytest.raises(TypeError):
+        ops.decode(q.float(), kv, bt, sl, cb, cb, R, R.half(), out, 4, 16, 0, 40, 0.1)
+    with pytest.raises(TypeError):
+        ops.decode(q, kv, bt.long(), sl, cb, cb, R, R.half(), out, 4, 16, 0, 40, 0.1)
+    with pytest.raises(ValueError):
+        ops.decode(q[:, :, :64].contiguous(), kv, bt, sl, cb, cb, R, R.half(), out, 4, 16, 0,
+                   40, 0.1)
+    with pytest.raises(ValueError):
+        ops.decode(q, kv, bt, sl, cb, cb, R, R.half(), out.cpu(), 4, 16, 0, 40, 0.1)
+    k = torch.zeros(3, 8, 128, dtype=torch.float16, device=gpu)
+    with pytest.raises(TypeError):
+        ops.encode(k.float(), k.float(), torch.zeros(3, dtype=torch.int32, device=gpu), kv, cb, cb)
+    with pytest.raises(ValueError):
+        ops.encode(k[:, :, :64].contiguous(), k[:, :, :64].contiguous(),
+                   torch.zeros(3, dtype=torch.int32, device=gpu), kv, cb, cb)
+    cu = torch.tensor([0, 3], dtype=torch.int32, device=gpu)
+    with pytest.raises(NotImplementedError):
+        fork.varlen_fwd(k, k, k, None, cu, cu, None, None, None, None, 3, 3, 0.1, 0.1, False,
+                        True, -1, -1, 0.0, False, 1, None)
+    torch.cuda.synchronize()
