@@ -67,6 +67,31 @@ constexpr int kLutBytes = 2 * 256 * kLutEntry;         // 4 KiB
 // from LDS every tile cost 2-3 % (dense / compressed kernel, config 3).
 constexpr int kPrefillLds = kLutOff + kLutBytes;
 
+// Dense source: the K tile is copied into LDS by the direct-to-LDS DMA, 256-
+// byte rows (no pad) with the 16-byte chunks of row k permuted: chunk c of key
+// k sits at chunk position c ^ (k & 15).  One DMA instruction moves four keys
+// (64 lanes x 16 bytes); the lane writing position p of key k reads global
+// chunk p ^ (k & 15), and the 16 lanes of an MFMA operand read (rows c32,
+// chunk 2S + u) then fall in 16 distinct bank groups.
+constexpr int kKRowDense = kD * 2;                      // 256
+
+typedef unsigned v4u32 __attribute__((ext_vector_type(4)));
+
+// One 16-byte-per-lane direct-to-LDS load: lane l's 16 bytes at rsrc+voff go
+// to LDS address lds_base + 16*l.  Issued through asm so the compiler does not
+// track these asynchronous LDS writes; completion is ordered by explicit vmcnt
+// waits.  M0 (the LDS base operand) is saved and restored around the load.
+__device__ __forceinline__ void dma_x4_to_lds(v4u32 rsrc, uint32_t voff, uint32_t lds_base) {
+    uint32_t saved;
+    asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %3\n\t"
+                 "buffer_load_dwordx4 %1, %2, 0 offen lds\n\ts_mov_b32 m0, %0"
+                 : "=&s"(saved) : "v"(voff), "s"(rsrc), "s"(lds_base) : "memory");
+}
+
+__device__ __forceinline__ uint32_t lds_addr32(const void *ptr) {
+    return (uint32_t)(size_t)(const __attribute__((address_space(3))) void *)ptr;
+}
+
 __device__ __forceinline__ floatx16 mfma32(half8 a, half8 b, floatx16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
 }
@@ -261,17 +286,11 @@ __device__ __forceinline__ void load_tile(const PrefillParams &p, TileRegs &r, T
         }
     } else {
         // Dense rows and the row pitch are below 2^31: 32 x 32 -> 64-bit multiplies.
+        // The K tile goes by DMA (issue_k_dma); only V passes through registers.
+        (void)tk;
+        (void)ck;
         const uint32_t r0 = (uint32_t)(dense_row0 + kbase);
         const uint32_t hs = (uint32_t)(p.H_kv * kD);
-        uint4 x0 = make_uint4(0, 0, 0, 0), x1 = x0;
-        if (tk < nk_valid) {
-            const uint4 *src =
-                reinterpret_cast<const uint4 *>(p.k_rot + (uint64_t)(r0 + tk) * hs + h * kD + 16 * ck);
-            x0 = src[0];
-            x1 = src[1];
-        }
-        r.k[0] = x0.x; r.k[1] = x0.y; r.k[2] = x0.z; r.k[3] = x0.w;
-        r.k[4] = x1.x; r.k[5] = x1.y; r.k[6] = x1.z; r.k[7] = x1.w;
         const uint16_t *vrow = p.v_rot + (uint64_t)(r0 + 4 * gv) * hs + h * kD + 4 * cv;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -328,7 +347,7 @@ __device__ __forceinline__ void store_tile(const TileRegs &r, uint8_t *kt, uint8
         }
     } else {
 #pragma unroll
-        for (int j = 0; j < 8; ++j) kw[j] = r.k[j];
+        for (int j = 0; j < 8; ++j) kw[j] = 0u;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             pr[i][0] = r.v[2 * i];
@@ -344,9 +363,11 @@ __device__ __forceinline__ void store_tile(const TileRegs &r, uint8_t *kt, uint8
         vw[k][0] = __builtin_amdgcn_perm(pr[1][w], pr[0][w], sel);
         vw[k][1] = __builtin_amdgcn_perm(pr[3][w], pr[2][w], sel);
     }
-    uint4 *kd = reinterpret_cast<uint4 *>(kt + tk * kKRow + 32 * ck);
-    kd[0] = make_uint4(kw[0], kw[1], kw[2], kw[3]);
-    kd[1] = make_uint4(kw[4], kw[5], kw[6], kw[7]);
+    if (PAGED) {
+        uint4 *kd = reinterpret_cast<uint4 *>(kt + tk * kKRow + 32 * ck);
+        kd[0] = make_uint4(kw[0], kw[1], kw[2], kw[3]);
+        kd[1] = make_uint4(kw[4], kw[5], kw[6], kw[7]);
+    }
     const uint32_t vo = v_key_off(gv);
 #pragma unroll
     for (int k = 0; k < 4; ++k)
@@ -456,6 +477,12 @@ prefill_kernel(PrefillParams p) {
     // rows 32*T + c32 (16 bytes at key group 2*sub + s, half u).
     const uint32_t k_lane = (uint32_t)(c32 * kKRow + 16 * u);
     const uint32_t v_lane = (uint32_t)(kKTile + c32 * kVRow + 16 * u);
+    // Dense source: byte offset of row c32, chunk 2S + u in the permuted K tile.
+    uint32_t k_off[8];
+#pragma unroll
+    for (int S = 0; S < 8; ++S)
+        k_off[S] = PAGED ? k_lane + 32u * S
+                         : (uint32_t)(c32 * kKRowDense + 16 * ((2 * S + u) ^ (c32 & 15)));
 
     // Per 64-key tile: S^T = K q_rot^T; online softmax in the log2 domain with
     // a lazy rescale (the running max moves only when a tile's max exceeds it
@@ -491,8 +518,9 @@ prefill_kernel(PrefillParams p) {
             for (int i = 0; i < 2; ++i) {
                 const int S = S0 + i;
                 qv[i] = qb[S];
-                a0[i] = *reinterpret_cast<const half8 *>(buf + k_lane + 32 * S);
-                a1[i] = *reinterpret_cast<const half8 *>(buf + k_lane + 32 * kKRow + 32 * S);
+                a0[i] = *reinterpret_cast<const half8 *>(buf + k_off[S]);
+                a1[i] = *reinterpret_cast<const half8 *>(
+                    buf + k_off[S] + 32 * (PAGED ? kKRow : kKRowDense));
             }
 #pragma unroll
             for (int i = 0; i < 2; ++i) {
@@ -578,8 +606,35 @@ prefill_kernel(PrefillParams p) {
     const int64_t dense_row0 = PAGED ? 0 : p.cu_k[b];
     TileRegs cur;
     TileRows rows_next{0, 0};
+    // Dense source: K tile j into LDS buffer j & 1 by DMA, two instructions per
+    // wave (keys 8*wave .. +7).  Keys past the end of the tile's valid range
+    // read the last valid key's row (in bounds; their scores are masked).
+    auto issue_k_dma = [&](int j) CDA_INLINE {
+        if constexpr (!PAGED) {
+            const int kb = j * kBN;
+            const int nk_valid = min(kBN, kend - kb);
+            const uint32_t pitch = (uint32_t)(p.H_kv * kD * 2);
+            const uint64_t base =
+                (uint64_t)(p.k_rot + ((uint64_t)(dense_row0 + kb) * p.H_kv + h) * kD);
+            const v4u32 r = {(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)base),
+                             (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(base >> 32)) & 0xFFFFu,
+                             (uint32_t)(kBN * pitch), 0x00020000u};
+            const uint32_t dst = __builtin_amdgcn_readfirstlane(lds_addr32(smem)) +
+                                 (uint32_t)((j & 1) * kTileBytes);
+#pragma unroll
+            for (int t = 0; t < 2; ++t) {
+                const int ins = 2 * wave + t;               // keys 4*ins .. 4*ins + 3
+                const int key = 4 * ins + (lane >> 4);
+                const int pos = lane & 15;
+                const uint32_t voff =
+                    (uint32_t)min(key, nk_valid - 1) * pitch + 16u * (uint32_t)(pos ^ (key & 15));
+                dma_x4_to_lds(r, voff, dst + 1024u * (uint32_t)ins);
+            }
+        }
+    };
     if (jt0 < jt1) {
         const int k0 = jt0 * kBN, k1 = k0 + kBN;
+        issue_k_dma(jt0);
         load_tile<PAGED>(p, cur, fetch_rows<PAGED>(p, bt_row, k0, min(kBN, kend - k0), tid),
                          dense_row0, h, k0, min(kBN, kend - k0), tid);
         if (jt0 + 1 < jt1) rows_next = fetch_rows<PAGED>(p, bt_row, k1, min(kBN, kend - k1), tid);
@@ -587,8 +642,12 @@ prefill_kernel(PrefillParams p) {
     __syncthreads();   // tables visible
 
     // Tile j into LDS (the whole workgroup), then the loads of tile j + 1.
+    // Dense source: the K DMA of tile j (issued after the previous barrier)
+    // and tile j's V loads are waited for here; the K DMA of tile j + 1 goes
+    // out after this barrier, when every wave is done with buffer (j + 1) & 1.
     auto produce = [&](int j) CDA_INLINE {
         uint8_t *buf = smem + (j & 1) * kTileBytes;
+        if constexpr (!PAGED) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         store_tile<PAGED>(cur, buf, buf + kKTile, lutk, lutv, tid);
         if (j + 1 < jt1) {
             const int k1 = (j + 1) * kBN, k2 = (j + 2) * kBN;
@@ -596,6 +655,7 @@ prefill_kernel(PrefillParams p) {
             if (j + 2 < jt1) rows_next = fetch_rows<PAGED>(p, bt_row, k2, min(kBN, kend - k2), tid);
         }
         __syncthreads();
+        if (j + 1 < jt1) issue_k_dma(j + 1);
         return buf;
     };
     // The tiles whole for every row of this wave come first, those crossing
