@@ -7,11 +7,13 @@
 A step is one K4V4 split-K decode over the paged cache (Llama-3-8B head
 shape: 32 Q / 8 KV heads, d=128, block 16, randomly permuted block table),
 from unrotated fp16 Q to unrotated fp16 O, with the cache already resident in
-HBM.  The timed region replays a captured hipGraph of the step K times
-between two synchronisations, after W untimed warm-up replays that follow a
-0.2-s settle phase of untimed replays (the GPU clocks take ~50 ms to ramp
-from idle; without it the first ~80 steps run ~10 % slow).  Prints ONE JSON
-line on stdout.
+HBM.  The timed region runs the step K times between two synchronisations,
+as direct calls of the public wrapper (``--launch graph``: replays of a
+captured hipGraph of it; both are timed and reported, a one-kernel graph
+replay costs ~7-11 us of GPU time of its own on this stack), after W untimed
+warm-up steps that follow a 0.2-s settle phase of untimed replays (the GPU
+clocks take ~50 ms to ramp from idle; without it the first ~80 steps run
+~10 % slow).  Prints ONE JSON line on stdout.
 
 * ``value`` = algorithmic HBM bytes per step / time per step (GB/s); the
   bytes are B*N*8*136 (codes + fp32 norms per token and KV head) + Q/O +
@@ -28,8 +30,10 @@ line on stdout.
   threads and one; ``c_checker`` beside it = the C checker
   (``oracle/cda_oracle.c``) on the same workload.
 ``--sweep`` also times the 3x3 grid B in {1,4,32} x N in {4K,16K,64K} (median
-of 20 graph replays after 5 warm-ups, as the reference's Table 2) and writes
-it to stderr (and as a JSON list to ``--sweep-out PATH`` when given).
+of 20 graph replays after 5 warm-ups, each bracketed by events on an idle GPU,
+as the reference's Table 2; ``queued_us_per_step`` is the same replay queued
+behind a short spin kernel, i.e. without the host's graph-launch latency) and
+writes it to stderr (and as a JSON list to ``--sweep-out PATH`` when given).
 """
 from __future__ import annotations
 
@@ -896,11 +900,62 @@ def replay_median_us(g, iters: int) -> float:
     return statistics.median(vals)
 
 
+def replay_queued_median_us(g, iters: int, spin_cycles: int = 200_000) -> float:
+    """Median GPU time of one replay of ``g`` queued behind a spin kernel.
+
+    Each replay is preceded by ``torch.cuda._sleep`` (a kernel that spins for
+    ``spin_cycles`` shader clocks, ~0.1 ms), so the host has submitted the
+    start event and the graph before the GPU reaches them: the events then
+    bracket the graph's own execution (its dispatches and the gaps between
+    them), not the host's graph-launch latency.  That is what a step costs in
+    a loop that enqueues steps back to back."""
+    import torch
+    vals = []
+    for _ in range(iters):
+        a = torch.cuda.Event(enable_timing=True)
+        b = torch.cuda.Event(enable_timing=True)
+        torch.cuda._sleep(spin_cycles)
+        a.record()
+        g.replay()
+        b.record()
+        torch.cuda.synchronize()
+        vals.append(a.elapsed_time(b) * 1000.0)
+    return statistics.median(vals)
+
+
+def direct_queued_us(fn, iters: int, spin_cycles: int = 2_000_000) -> float:
+    """GPU time per step of ``iters`` back-to-back direct calls of ``fn``.
+
+    A spin kernel of ``spin_cycles`` shader clocks (~1 ms) runs first, so the
+    host has queued the calls before the GPU reaches the start event; the
+    events then bracket the steps' own execution and the gaps between their
+    dispatches."""
+    import torch
+    fn()
+    torch.cuda.synchronize()
+    a = torch.cuda.Event(enable_timing=True)
+    b = torch.cuda.Event(enable_timing=True)
+    torch.cuda._sleep(spin_cycles)
+    a.record()
+    for _ in range(iters):
+        fn()
+    b.record()
+    torch.cuda.synchronize()
+    return a.elapsed_time(b) * 1000.0 / iters
+
+
 def split_kernel_us(fn, iters: int) -> float:
-    """Average duration of the split-K kernel alone (HIP events on its stream)."""
+    """Average duration of the split-K kernel alone (HIP events that the
+    library records on its launch stream right around that kernel).  A spin
+    kernel (~1 ms) is queued first, so the host has enqueued the calls before
+    the GPU reaches them and no host latency falls between an event and its
+    kernel."""
     import torch
     from sub0_amd import _native
     pairs = []
+    fn()
+    torch.cuda.synchronize()
+    torch.cuda._sleep(2_000_000)
     for _ in range(iters):
         a = torch.cuda.Event(enable_timing=True)
         b = torch.cuda.Event(enable_timing=True)
@@ -1059,6 +1114,9 @@ def main(argv=None):
     ap.add_argument("--B", type=int, default=32)
     ap.add_argument("--N", type=int, default=65536)
     ap.add_argument("--sweep", action="store_true")
+    ap.add_argument("--launch", choices=("direct", "graph"), default="direct",
+                    help="how the timed decode steps are launched: direct calls of the public "
+                         "wrapper (default) or replays of a captured hipGraph")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--tile-n", type=int, default=0,
                     help="tokens per split-K partition (0 = the library's plan)")
@@ -1144,15 +1202,25 @@ def main(argv=None):
     fn = decode_call(w, args.tile_n)
     g = capture(fn, args.warmup)
     settle(g)
-    for _ in range(args.warmup):
-        g.replay()
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        g.replay()
-    torch.cuda.synchronize()
-    t1 = time.perf_counter()
-    ms_per_step = (t1 - t0) / args.steps * 1e3
+
+    def timed(step) -> float:
+        """ms per step over args.steps back-to-back calls of ``step``."""
+        for _ in range(args.warmup):
+            step()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            step()
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) / args.steps * 1e3
+
+    # A hipGraph replay costs ~7-11 us of GPU time of its own on this stack
+    # (a one-kernel graph 13 us queued against 6 us for the same kernel launched
+    # directly), so the step is launched directly, through the public wrapper,
+    # unless --launch graph; the other form is timed and reported beside it.
+    ms_graph = timed(g.replay)
+    ms_direct = timed(fn)
+    ms_per_step = ms_graph if args.launch == "graph" else ms_direct
     med_us = replay_median_us(g, 20)
     k_us = split_kernel_us(fn, max(5, args.steps))
     slot_data = 104 if args.k4v2 else (136 if levels == 16 else 72)
@@ -1172,11 +1240,17 @@ def main(argv=None):
                 g2 = capture(f2, 5)
                 settle(g2, 0.05)
                 us = replay_median_us(g2, 20)
+                qus = replay_queued_median_us(g2, 20)
+                dus = direct_queued_us(f2, 20)
                 kus = split_kernel_us(f2, 20)
                 nb2 = _native.decode_algorithmic_bytes(sb, sn)
                 row = dict(B=sb, N=sn, us_per_step=round(us, 2),
                            gbs=round(nb2 / (us * 1e-6) / 1e9, 1),
                            pct_peak=round(100 * nb2 / (us * 1e-6) / 1e9 / PEAK_GBS, 1),
+                           queued_us_per_step=round(qus, 2),
+                           queued_pct_peak=round(100 * nb2 / (qus * 1e-6) / 1e9 / PEAK_GBS, 1),
+                           direct_us_per_step=round(dus, 2),
+                           direct_pct_peak=round(100 * nb2 / (dus * 1e-6) / 1e9 / PEAK_GBS, 1),
                            split_kernel_us=round(kus, 2),
                            split_gbs=round(nb2 / (kus * 1e-6) / 1e9, 1),
                            bytes=nb2, tile_n=_native.decode_plan(sb, H_Q, H_KV, sn)[0],
@@ -1225,6 +1299,9 @@ def main(argv=None):
         "warmup": args.warmup,
         "ms_per_step": round(ms_per_step, 5),
         "us_per_step": round(ms_per_step * 1e3, 2),
+        "launch": args.launch,
+        "us_per_step_direct": round(ms_direct * 1e3, 2),
+        "us_per_step_graph": round(ms_graph * 1e3, 2),
         "us_per_step_median_replay": round(med_us, 2),
         "pct_of_hbm_peak": round(100 * value / PEAK_GBS, 1),
         "higher_is_better": True,
