@@ -318,6 +318,18 @@ int cda_fa2_varlen_fwd(const void *q, const void *k, const void *v, void *out,
                        const int32_t *seqused_k, int B, int T, int H_q, int H_kv,
                        int max_query_len, float scale, int causal, void *stream);
 
+/* cda_fa2_varlen_fwd_lse: cda_fa2_varlen_fwd that also writes the softmax
+ * log-sum-exp the fork's varlen ops return beside out
+ * (cda/kernels_vllm_fa2_fork/interface.py:234-258, 304-329, 434-470):
+ * softmax_lse (H_q, T) fp32, softmax_lse[h][t] = log(sum over query t's
+ * visible keys of exp(scale * q.k)), +inf for a query with no visible key
+ * (FlashAttention-2's varlen layout and convention). */
+int cda_fa2_varlen_fwd_lse(const void *q, const void *k, const void *v, void *out,
+                           const int32_t *cu_seqlens_q, const int32_t *cu_seqlens_k,
+                           const int32_t *seqused_k, int B, int T, int H_q, int H_kv,
+                           int max_query_len, float scale, int causal, float *softmax_lse,
+                           void *stream);
+
 /* cda_dequantize_rows: out row r = fp16(cb[code] * norm) (compression.py:
  * 337-361, rotated frame) of code rows (rows, H, 64 or 32 bytes) and norms
  * (rows, H) fp32 -- the reference fork's dequantize_compressed_kv for one of

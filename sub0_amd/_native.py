@@ -41,6 +41,7 @@ SYMBOLS = (
     "cda_prefill_paged_hadamard_ws",
     "cda_fa2_varlen_fwd_hadamard",
     "cda_fa2_varlen_fwd",
+    "cda_fa2_varlen_fwd_lse",
     "cda_dequantize_rows",
     "cda_fa2_paged_cache_to_dense_rotated",
     "cda_hadamard128_fp16",
@@ -153,6 +154,9 @@ def lib():
         L.cda_fa2_varlen_fwd.restype = _I32
         L.cda_fa2_varlen_fwd.argtypes = [
             _P, _P, _P, _P, _P, _P, _P, _I32, _I32, _I32, _I32, _I32, _F32, _I32, _P]
+        L.cda_fa2_varlen_fwd_lse.restype = _I32
+        L.cda_fa2_varlen_fwd_lse.argtypes = [
+            _P, _P, _P, _P, _P, _P, _P, _I32, _I32, _I32, _I32, _I32, _F32, _I32, _P, _P]
         L.cda_dequantize_rows.restype = _I32
         L.cda_dequantize_rows.argtypes = [
             _P, _P, _I64, _I32, _P, _I32, _P, _I32, _P, _I32, _I32, _P, _P]
@@ -545,12 +549,19 @@ def fa2_varlen_fwd_hadamard(q: torch.Tensor, k_rot: torch.Tensor, v_rot: torch.T
 def fa2_varlen_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, out: torch.Tensor,
                    cu_seqlens_q: torch.Tensor, cu_seqlens_k: torch.Tensor,
                    seqused_k: torch.Tensor, max_query_len: int, scale: float,
-                   causal: bool) -> None:
+                   causal: bool, softmax_lse: torch.Tensor | None = None) -> None:
     """Varlen flash attention over dense fp16 K/V rows with no rotation: q, k,
     v and out all in one frame (the FA2 varlen forward the fork's
     comparator ops run).  Sequence b's keys are rows cu_seqlens_k[b] ..
-    cu_seqlens_k[b] + seqused_k[b] - 1; causal = bottom-right aligned."""
+    cu_seqlens_k[b] + seqused_k[b] - 1; causal = bottom-right aligned.
+    With ``softmax_lse`` ((H_q, T) fp32) it also receives each query's
+    log(sum exp(scale * q.k)) over its visible keys, +inf where none."""
     dev = _require_gpu(q, k, v, out, cu_seqlens_q, cu_seqlens_k, seqused_k)
+    if softmax_lse is not None:
+        _require_gpu(q, softmax_lse)
+        if (softmax_lse.dtype != torch.float32 or not softmax_lse.is_contiguous()
+                or tuple(softmax_lse.shape) != (q.shape[1], q.shape[0])):
+            raise ValueError("softmax_lse must be a contiguous (H_q, T) fp32 tensor")
     for t, nm in ((q, "q"), (k, "k"), (v, "v"), (out, "out")):
         if t.dtype != torch.float16:
             raise TypeError(f"{nm} must be fp16")
@@ -564,6 +575,13 @@ def fa2_varlen_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, out: torch
             raise TypeError(f"{nm} must be int32")
     T, H_q, _ = q.shape
     B = cu_seqlens_q.numel() - 1
+    if softmax_lse is not None:
+        rc = lib().cda_fa2_varlen_fwd_lse(
+            _ptr(q), _ptr(k), _ptr(v), _ptr(out), _ptr(cu_seqlens_q), _ptr(cu_seqlens_k),
+            _ptr(seqused_k), B, T, H_q, k.shape[1], int(max_query_len), float(scale),
+            int(bool(causal)), _ptr(softmax_lse), _stream(dev))
+        _check(rc, "cda_fa2_varlen_fwd_lse")
+        return
     rc = lib().cda_fa2_varlen_fwd(
         _ptr(q), _ptr(k), _ptr(v), _ptr(out), _ptr(cu_seqlens_q), _ptr(cu_seqlens_k),
         _ptr(seqused_k), B, T, H_q, k.shape[1], int(max_query_len), float(scale),

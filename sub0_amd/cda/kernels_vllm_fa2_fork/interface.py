@@ -16,8 +16,10 @@ reference (``interface.py:138-470``):
 
 Differences, all explicit: inference only (dropout 0), no sliding window,
 soft-capping, ALiBi, split-KV, FP8 descales or sink tokens
-(``NotImplementedError``, as the reference for most of them); the softmax LSE
-is not produced (``return_softmax_lse=True`` raises); ``gqa_decode_swap`` is
+(``NotImplementedError``, as the reference for most of them);
+``return_softmax_lse=True`` returns ``(out, softmax_lse)`` as the reference,
+softmax_lse (H_q, total_q) fp32 (log of the sum of exp(scale * q.k) over each
+query's visible keys, +inf where there are none); ``gqa_decode_swap`` is
 accepted and has no effect (the varlen kernel serves a GQA group from one K/V
 tile already); ``flash_attn_varlen_func`` takes contiguous K/V only (no
 ``block_table``).
@@ -45,11 +47,9 @@ def _window(window_size: Sequence[int] | None) -> tuple[int, int]:
     return int(window_size[0]), int(window_size[1])
 
 
-def _inference_args(dropout_p: float, return_softmax_lse: bool, softmax_scale, head_dim: int):
+def _inference_args(dropout_p: float, softmax_scale, head_dim: int):
     if dropout_p != 0.0:
         raise NotImplementedError("inference only: dropout_p must be 0")
-    if return_softmax_lse:
-        raise NotImplementedError("the softmax LSE is not produced by this build")
     return float(softmax_scale) if softmax_scale is not None else head_dim ** -0.5
 
 
@@ -123,7 +123,7 @@ def flash_attn_varlen_func(
     if any(d is not None and t.dtype in fp8 for t, d in ((q, q_descale), (k, k_descale),
                                                           (v, v_descale))):
         raise NotImplementedError("FP8 inputs are not supported")
-    scale = _inference_args(dropout_p, return_softmax_lse, softmax_scale, q.shape[-1])
+    scale = _inference_args(dropout_p, softmax_scale, q.shape[-1])
     wl, wr = _window(window_size)
     if cu_seqlens_k is None:
         # The reference reaches K through block_table in this case.
@@ -133,7 +133,7 @@ def flash_attn_varlen_func(
                             alibi_slopes, int(max_seqlen_q), int(max_seqlen_k), 0.0, scale,
                             False, bool(causal), wl, wr, float(softcap), False, int(num_splits),
                             None)
-    return res[0]
+    return (res[0], res[1]) if return_softmax_lse else res[0]
 
 
 def flash_attn_varlen_compressed_kv_func(
@@ -148,7 +148,7 @@ def flash_attn_varlen_compressed_kv_func(
 ) -> torch.Tensor:
     """Compressed K/V (rotated frame) dequantised to fp16 rows, then the
     varlen attention: the two-step bridge."""
-    scale = _inference_args(dropout_p, return_softmax_lse, softmax_scale, q.shape[-1])
+    scale = _inference_args(dropout_p, softmax_scale, q.shape[-1])
     wl, wr = _window(window_size)
     ki, kn, vi, vn = _pair(k_idx, k_norm, v_idx, v_norm)
     res = _ops().varlen_fwd_compressed_kv(q, ki, kn, vi, vn, cb_k.contiguous(),
@@ -156,7 +156,7 @@ def flash_attn_varlen_compressed_kv_func(
                                           alibi_slopes, int(max_seqlen_q), int(max_seqlen_k),
                                           0.0, scale, False, bool(causal), wl, wr,
                                           float(softcap), False, int(num_splits), None)
-    return res[0]
+    return (res[0], res[1]) if return_softmax_lse else res[0]
 
 
 def flash_attn_varlen_compressed_kv_fused_func(
@@ -174,7 +174,7 @@ def flash_attn_varlen_compressed_kv_fused_func(
     block_size, H_kv, D/2) + (num_blocks, block_size, H_kv) with
     ``block_table`` and ``seqused_k``."""
     del gqa_decode_swap
-    scale = _inference_args(dropout_p, return_softmax_lse, softmax_scale, q.shape[-1])
+    scale = _inference_args(dropout_p, softmax_scale, q.shape[-1])
     wl, wr = _window(window_size)
     if block_table is not None:
         if seqused_k is None:
@@ -197,7 +197,7 @@ def flash_attn_varlen_compressed_kv_fused_func(
         cu_seqlens_k, seqused_k, block_table, alibi_slopes, int(max_seqlen_q),
         int(max_seqlen_k), 0.0, scale, False, bool(causal), wl, wr, float(softcap), False,
         int(num_splits), bool(uniform_codebook), None)
-    return res[0]
+    return (res[0], res[1]) if return_softmax_lse else res[0]
 
 
 def register_vllm_backend(slot: str = "CUSTOM") -> None:

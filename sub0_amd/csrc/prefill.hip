@@ -208,6 +208,10 @@ struct PrefillParams {
     // partial over other keys of the same queries (written by an earlier
     // launch), merged in before the epilogue (attention.py:239-272).
     int merge_slot0;
+    // Unsplit kernel only: when set, lse[hq * T_total + t] = the natural-log
+    // sum of exp(scale * q.k) over query t's visible keys (FlashAttention-2's
+    // varlen softmax_lse layout), +inf for a query with no visible key.
+    float *lse;
 };
 constexpr int kKeysAll = 0, kKeysPast = 1, kKeysChunk = 2;
 
@@ -725,6 +729,13 @@ prefill_kernel(PrefillParams p) {
             }
     }
 
+    if (p.lse != nullptr && u == 0 && qw0 + c32 < seq_q && q_begin + qw0 + c32 < p.T_total) {
+        // m_run is the running max of scale * s * log2(e); l_run sums 2^(that - m_run).
+        constexpr float kLn2 = 0.6931471805599453f;
+        p.lse[(int64_t)hq * p.T_total + q_begin + qw0 + c32] =
+            l_run > 0.0f ? (m_run + log2f(l_run)) * kLn2 : INFINITY;
+    }
+
     // ---- epilogue: O_rot = fp16(O / l) (attention.py:93), out = fp16(O_rot H / sqrt(128)).
     const float inv_l = 1.0f / fmaxf(l_run, 1e-30f);
     half8 ob[8];
@@ -1143,8 +1154,8 @@ namespace {
 int fa2_varlen_dense(const void *q, const void *k, const void *v, void *out,
                      const int32_t *cu_seqlens_q, const int32_t *cu_seqlens_k,
                      const int32_t *seqused_k, int B, int T, int H_q, int H_kv,
-                     int max_query_len, float scale, int causal, int rotate, void *stream,
-                     const char *fn) {
+                     int max_query_len, float scale, int causal, int rotate, float *lse,
+                     void *stream, const char *fn) {
     const std::string f(fn);
     CDA_REQUIRE(q && k && v && out && cu_seqlens_q && cu_seqlens_k && seqused_k,
                 f + ": null pointer argument");
@@ -1173,6 +1184,7 @@ int fa2_varlen_dense(const void *q, const void *k, const void *v, void *out,
     p.T_total = T;
     p.rotate = rotate;
     p.causal = causal;
+    p.lse = lse;
     return launch_prefill<false>(p, B, max_query_len, static_cast<hipStream_t>(stream), fn);
 }
 
@@ -1247,7 +1259,7 @@ extern "C" int cda_fa2_varlen_fwd_hadamard(const void *q, const void *k_rot, con
                                            int max_seq_len, float scale, void *stream) {
     (void)max_seq_len;
     return fa2_varlen_dense(q, k_rot, v_rot, out, cu_seqlens_q, cu_seqlens_k, seqused_k, B, T,
-                            H_q, H_kv, max_query_len, scale, 1, 1, stream,
+                            H_q, H_kv, max_query_len, scale, 1, 1, nullptr, stream,
                             "cda_fa2_varlen_fwd_hadamard");
 }
 
@@ -1256,7 +1268,19 @@ extern "C" int cda_fa2_varlen_fwd(const void *q, const void *k, const void *v, v
                                   const int32_t *seqused_k, int B, int T, int H_q, int H_kv,
                                   int max_query_len, float scale, int causal, void *stream) {
     return fa2_varlen_dense(q, k, v, out, cu_seqlens_q, cu_seqlens_k, seqused_k, B, T, H_q, H_kv,
-                            max_query_len, scale, causal != 0, 0, stream, "cda_fa2_varlen_fwd");
+                            max_query_len, scale, causal != 0, 0, nullptr, stream,
+                            "cda_fa2_varlen_fwd");
+}
+
+extern "C" int cda_fa2_varlen_fwd_lse(const void *q, const void *k, const void *v, void *out,
+                                      const int32_t *cu_seqlens_q, const int32_t *cu_seqlens_k,
+                                      const int32_t *seqused_k, int B, int T, int H_q, int H_kv,
+                                      int max_query_len, float scale, int causal,
+                                      float *softmax_lse, void *stream) {
+    CDA_REQUIRE(softmax_lse != nullptr, "cda_fa2_varlen_fwd_lse: softmax_lse is null");
+    return fa2_varlen_dense(q, k, v, out, cu_seqlens_q, cu_seqlens_k, seqused_k, B, T, H_q, H_kv,
+                            max_query_len, scale, causal != 0, 0, softmax_lse, stream,
+                            "cda_fa2_varlen_fwd_lse");
 }
 
 extern "C" int cda_dequantize_rows(const void *codes, const float *norms, int64_t rows, int H,

@@ -490,17 +490,27 @@ Tensor seqused_of(const Tensor &cu_k, const c10::optional<Tensor> &seqused) {
     return (cu_k.slice(0, 1) - cu_k.slice(0, 0, cu_k.numel() - 1)).to(at::kInt).contiguous();
 }
 
-// Returns [out, softmax_lse]; the fork fills softmax_lse only for
-// return_softmax with dropout, which inference never uses, so it is empty.
+// Returns [out, softmax_lse] as the fork's varlen ops do: softmax_lse is
+// (H_q, total_q) fp32, the natural-log sum of exp(scale * q.k) over each
+// query's visible keys (+inf where it sees none).
 std::vector<Tensor> attend(const Tensor &q, const Tensor &k, const Tensor &v,
                            const c10::optional<Tensor> &out_opt, const Tensor &cu_q,
                            const Tensor &cu_k, const Tensor &seqused, int64_t max_q,
                            double scale, bool causal) {
     Tensor out = out_opt.has_value() ? *out_opt : at::empty_like(q);
     const Tensor cq = cu_q.to(at::kInt).contiguous(), ckk = cu_k.to(at::kInt).contiguous();
-    varlen_fwd(q.contiguous(), k.contiguous(), v.contiguous(), out, cq, ckk, seqused, max_q,
-               scale, causal);
-    return {out, at::empty({0}, q.options().dtype(at::kFloat))};
+    const Tensor qc = q.contiguous(), kc = k.contiguous(), vc = v.contiguous();
+    const DeviceGuard guard(on_gpu({&qc, &kc, &vc, &out, &cq, &ckk, &seqused}));
+    check_dense_attn(qc, kc, vc, out, cq, ckk, seqused, "q", "k", "v", "out");
+    Tensor lse = at::empty({qc.size(1), qc.size(0)}, qc.options().dtype(at::kFloat));
+    check_rc(cda_fa2_varlen_fwd_lse(qc.data_ptr(), kc.data_ptr(), vc.data_ptr(), out.data_ptr(),
+                                    cq.data_ptr<int32_t>(), ckk.data_ptr<int32_t>(),
+                                    seqused.data_ptr<int32_t>(), (int)cq.numel() - 1,
+                                    (int)qc.size(0), (int)qc.size(1), (int)kc.size(1),
+                                    (int)max_q, (float)scale, causal ? 1 : 0,
+                                    lse.data_ptr<float>(), stream_of(qc)),
+             "cda_fa2_varlen_fwd_lse");
+    return {out, lse};
 }
 
 std::vector<Tensor> fork_varlen_fwd(const Tensor &q, const Tensor &k, const Tensor &v,
@@ -605,7 +615,8 @@ std::tuple<Tensor, Tensor> meta_dequantize(const Tensor &k_idx, const Tensor &, 
 }
 
 std::vector<Tensor> meta_fork_out(const Tensor &q, const c10::optional<Tensor> &out) {
-    return {out.has_value() ? *out : at::empty_like(q), at::empty({0}, q.options().dtype(at::kFloat))};
+    return {out.has_value() ? *out : at::empty_like(q),
+            at::empty({q.size(1), q.size(0)}, q.options().dtype(at::kFloat))};
 }
 
 std::vector<Tensor> meta_fork_varlen(const Tensor &q, const Tensor &, const Tensor &,

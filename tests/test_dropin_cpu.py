@@ -126,6 +126,21 @@ def test_fa2_fork_build_stub():
     assert hasattr(torch.ops._cda_vllm_fa2_fork_C, "varlen_fwd")
 
 
+def test_fa2_fork_varlen_returns_lse_shape_on_meta():
+    """The fork's varlen op returns (out, softmax_lse) with softmax_lse in
+    FlashAttention-2's varlen layout (H_q, total_q) fp32 (reference
+    interface.py:234-258); the meta kernel gives the shapes without a GPU."""
+    from sub0_amd.cda._prebuilt_loader import load_torch_ops_library
+    fork = load_torch_ops_library("_cda_vllm_fa2_fork_C")
+    q = torch.empty(6, 8, 128, dtype=torch.float16, device="meta")
+    k = torch.empty(6, 2, 128, dtype=torch.float16, device="meta")
+    cu = torch.empty(3, dtype=torch.int32, device="meta")
+    out, lse = fork.varlen_fwd(q, k, k, None, cu, cu, None, None, None, None, 4, 4, 0.0, 0.1,
+                               False, True, -1, -1, 0.0, False, 0, None)
+    assert tuple(out.shape) == (6, 8, 128) and out.dtype == torch.float16
+    assert tuple(lse.shape) == (8, 6) and lse.dtype == torch.float32
+
+
 def test_fa2_fork_interface_rejects_unsupported():
     """The argument checks of kernels_vllm_fa2_fork's Python entry points
     (reference interface.py:200-217, 367-372) and this build's explicit
@@ -144,8 +159,6 @@ def test_fa2_fork_interface_rejects_unsupported():
         F.flash_attn_varlen_func(q, k, k, 4, cu, 4, cu_seqlens_k=cu, fa_version=3)
     with pytest.raises(NotImplementedError, match="dropout"):
         F.flash_attn_varlen_func(q, k, k, 4, cu, 4, cu_seqlens_k=cu, dropout_p=0.1)
-    with pytest.raises(NotImplementedError, match="LSE"):
-        F.flash_attn_varlen_func(q, k, k, 4, cu, 4, cu_seqlens_k=cu, return_softmax_lse=True)
     with pytest.raises(ValueError, match="exactly two"):
         F.flash_attn_varlen_func(q, k, k, 4, cu, 4, cu_seqlens_k=cu, window_size=(1,))
     ki = torch.zeros(4, 2, 64, dtype=torch.uint8)

@@ -228,3 +228,58 @@ def test_native_ops_error_types(gpu):
         fork.varlen_fwd(k, k, k, None, cu, cu, None, None, None, None, 3, 3, 0.1, 0.1, False,
                         True, -1, -1, 0.0, False, 1, None)
     torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("causal,scale", [(True, None), (False, None), (False, -0.05)])
+def test_fork_softmax_lse(gpu, causal, scale):
+    """return_softmax_lse=True (reference interface.py:234-258): out and the
+    (H_q, total_q) fp32 softmax_lse = log(sum exp(scale * q.k)) over each
+    query's visible keys, against fp32 torch.logsumexp; a sequence with more
+    queries than keys leaves its first causal rows with no visible key, which
+    get out = 0 and lse = +inf (FlashAttention-2's convention).  Tolerance
+    1e-3 on lse: the kernel sums the fp16-rounded weights (relative error
+    <= 2^-11 per term, <= 5e-4 after the log)."""
+    from sub0_amd.cda import kernels_vllm_fa2_fork as F
+    H_kv, H_q = 8, 32
+    lens, qlens = [300, 97, 1000, 20], [37, 1, 64, 40]
+    q = _t(synth.normal_f16(8500, (sum(qlens), H_q, 128)), gpu)
+    k = _t(synth.normal_f16(8501, (sum(lens), H_kv, 128)), gpu)
+    v = _t(synth.normal_f16(8502, (sum(lens), H_kv, 128)), gpu)
+    cu_q = torch.tensor(np.concatenate([[0], np.cumsum(qlens)]), dtype=torch.int32, device=gpu)
+    cu_k = torch.tensor(np.concatenate([[0], np.cumsum(lens)]), dtype=torch.int32, device=gpu)
+    sc = float(1 / np.sqrt(128)) if scale is None else scale
+    print(f"[torch-ops] fork softmax_lse causal={causal} scale={sc}", flush=True)
+    out, lse = F.flash_attn_varlen_func(q, k, v, max(qlens), cu_q, max(lens), cu_seqlens_k=cu_k,
+                                        causal=causal, softmax_scale=scale,
+                                        return_softmax_lse=True)
+    torch.cuda.synchronize()
+    assert tuple(lse.shape) == (H_q, sum(qlens)) and lse.dtype == torch.float32
+    ref_out = torch.zeros_like(q, dtype=torch.float32)
+    ref_lse = torch.empty(H_q, sum(qlens), dtype=torch.float32, device=gpu)
+    g = H_q // H_kv
+    cq = cu_q.tolist()
+    k0 = 0
+    for b, L in enumerate(lens):
+        qs = q[cq[b]:cq[b + 1]].float()
+        ks = k[k0:k0 + L].float().repeat_interleave(g, dim=1)
+        vs = v[k0:k0 + L].float().repeat_interleave(g, dim=1)
+        s = torch.einsum("mhd,khd->hmk", qs, ks) * sc
+        if causal:
+            M = qs.shape[0]
+            mask = torch.arange(L, device=gpu)[None, :] <= (
+                torch.arange(M, device=gpu)[:, None] + L - M)
+            s = s.masked_fill(~mask[None], float("-inf"))
+        lb = torch.logsumexp(s, dim=-1)                          # (H_q, M)
+        empty = torch.isinf(lb) & (lb < 0)
+        p = torch.softmax(s, dim=-1).nan_to_num(0.0)
+        ref_out[cq[b]:cq[b + 1]] = torch.einsum("hmk,khd->mhd", p, vs)
+        ref_lse[:, cq[b]:cq[b + 1]] = torch.where(empty, torch.full_like(lb, float("inf")), lb)
+        k0 += L
+    fin = torch.isfinite(ref_lse)
+    assert torch.equal(fin, torch.isfinite(lse)), "rows with no visible key must read +inf"
+    assert bool((lse[~fin] == float("inf")).all())
+    assert (int((~fin).sum()) > 0) == causal
+    err_lse = float((lse[fin] - ref_lse[fin]).abs().max())
+    err_out = float((out.float() - ref_out).abs().max())
+    assert err_lse <= 1e-3, err_lse
+    assert err_out <= TOL, err_out
