@@ -497,7 +497,7 @@ std::vector<Tensor> attend(const Tensor &q, const Tensor &k, const Tensor &v,
                            const c10::optional<Tensor> &out_opt, const Tensor &cu_q,
                            const Tensor &cu_k, const Tensor &seqused, int64_t max_q,
                            double scale, bool causal) {
-    Tensor out = out_opt.has_value() ? *out_opt : at::empty_like(q);
+    Tensor out = out_opt.has_value() ? *out_opt : at::empty(q.sizes(), q.options());
     const Tensor cq = cu_q.to(at::kInt).contiguous(), ckk = cu_k.to(at::kInt).contiguous();
     const Tensor qc = q.contiguous(), kc = k.contiguous(), vc = v.contiguous();
     const DeviceGuard guard(on_gpu({&qc, &kc, &vc, &out, &cq, &ckk, &seqused}));
